@@ -1,0 +1,218 @@
+// KV quantize-and-write: fp16/bf16 K and V rows -> int8 K codes, packed
+// int4 V codes and fp32 planes inside the paged cache.
+//
+// Reference: k8v4_v030/native/xe2_kv_ops.cpp:536-627 (two kernels, fp32
+// arithmetic with rint) and the parity oracle k8v4_v030/oracle.py:18-69
+// (float64, half-away-from-zero for K, floor(x+0.5) for V).  This kernel
+// follows the oracle: every rounding step is the same IEEE double operation
+// in the same order, so codes and stored scales are bit-identical to it.
+// This file is compiled with -ffp-contract=off and the kernel body disables
+// contraction as well, so no multiply-add is fused.
+//
+// Mapping (MI355X): K and V of one (token, kv_head) pair are handled by the
+// same D/8 lanes, 8 consecutive dims per lane (one 16-byte load of K and one
+// of V).  Consecutive pairs are consecutive heads of a token, so a wave
+// writes whole contiguous rows of a page: the store is one pass over the
+// inputs and one pass over the outputs, HBM-bound.
+#include "k8v4_common.h"
+
+namespace k8v4 {
+namespace {
+
+struct StoreArgs {
+  const uint16_t *k;
+  const uint16_t *v;
+  int64_t k_tok_stride;  // elements
+  int64_t v_tok_stride;
+  const int64_t *slots;
+  int64_t units;  // ntok * hkv
+  int8_t *k_cache;
+  float *k_scale;
+  uint8_t *v_cache;
+  float *v_scale;
+  float *v_zero;
+  int64_t num_pages;
+  int64_t k_ps, ks_ps, v_ps, vs_ps, vz_ps;  // page strides, bytes
+  int hkv;
+  int bf16;
+  int vec_ok;  // 16-byte aligned rows: one vector load per lane
+};
+
+__device__ __forceinline__ void load8(const uint16_t *src, bool vec_ok, bool bf16, float out[8]) {
+  uint16_t h[8];
+  if (vec_ok) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(src);
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[2 * i] = static_cast<uint16_t>(words[i] & 0xFFFFu);
+      h[2 * i + 1] = static_cast<uint16_t>(words[i] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = src[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = half_bits_to_float(h[i], bf16);
+}
+
+// Max / min over the LPU lanes of one (token, head) group.
+template <int LPU>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+  for (int m = 1; m < LPU; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, kWave));
+  return x;
+}
+template <int LPU>
+__device__ __forceinline__ float group_min(float x) {
+#pragma unroll
+  for (int m = 1; m < LPU; m <<= 1) x = fminf(x, __shfl_xor(x, m, kWave));
+  return x;
+}
+
+// One wave handles 64/LPU (token, head) pairs; LPU = D/8 lanes per pair.
+template <int D>
+__global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
+#pragma clang fp contract(off)
+  constexpr int LPU = D / 8;
+  constexpr int UPW = kWave / LPU;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const int sub = lane % LPU;
+  int64_t unit = wave * UPW + lane / LPU;
+  const bool live = unit < a.units;
+  if (!live) unit = a.units - 1;  // keep the group's shuffles on real data
+  const int64_t token = unit / a.hkv;
+  const int head = static_cast<int>(unit - token * a.hkv);
+
+  float kx[8], vx[8];
+  load8(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + 8 * sub, a.vec_ok, a.bf16, kx);
+  load8(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + 8 * sub, a.vec_ok, a.bf16, vx);
+
+  float amax = 0.f, lo = vx[0], hi = vx[0];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    amax = fmaxf(amax, fabsf(kx[i]));
+    lo = fminf(lo, vx[i]);
+    hi = fmaxf(hi, vx[i]);
+  }
+  amax = group_max<LPU>(amax);
+  lo = group_min<LPU>(lo);
+  hi = group_max<LPU>(hi);
+
+  const int64_t slot = a.slots[token];
+  const int64_t page = slot >= 0 ? slot / kPage : -1;
+  if (!live || page < 0 || page >= a.num_pages) return;
+  const int64_t row = slot - page * kPage;
+  const int64_t cell = row * a.hkv + head;
+
+  // K: symmetric int8, scale amax/127, round half away from zero.
+  const double k_scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
+  uint32_t kw[2] = {0u, 0u};
+  if (amax != 0.f) {
+    const double inv = 1.0 / k_scale;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const double y = static_cast<double>(kx[i]) * inv;
+      double q = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
+      q = fmin(fmax(q, -127.0), 127.0);
+      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xFFu;
+      kw[i >> 2] |= b << (8 * (i & 3));
+    }
+  }
+
+  // V: affine uint4 over the whole row, floor(x + 0.5) rounding.
+  const double lo_d = lo, hi_d = hi;
+  const double span = (hi_d - lo_d) / 15.0;
+  const double v_scale = span >= 1.0e-8 ? span : 1.0e-8;
+  const double zero = fmin(fmax(floor(-lo_d / v_scale + 0.5), 0.0), 15.0);
+  uint32_t vw = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    double q = floor(static_cast<double>(vx[i]) / v_scale + zero + 0.5);
+    q = fmin(fmax(q, 0.0), 15.0);
+    vw |= static_cast<uint32_t>(q) << (4 * i);
+  }
+
+  char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + 8 * sub;
+  *reinterpret_cast<uint2 *>(kdst) = make_uint2(kw[0], kw[1]);
+  char *vdst = reinterpret_cast<char *>(a.v_cache) + page * a.v_ps + cell * (D / 2) + 4 * sub;
+  *reinterpret_cast<uint32_t *>(vdst) = vw;
+  if (sub == 0) {
+    *reinterpret_cast<float *>(reinterpret_cast<char *>(a.k_scale) + page * a.ks_ps + cell * 4) =
+        static_cast<float>(k_scale);
+    *reinterpret_cast<float *>(reinterpret_cast<char *>(a.v_scale) + page * a.vs_ps + cell * 4) =
+        static_cast<float>(v_scale);
+    *reinterpret_cast<float *>(reinterpret_cast<char *>(a.v_zero) + page * a.vz_ps + cell * 4) =
+        static_cast<float>(zero);
+  }
+}
+
+bool aligned(const void *p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
+                                   int64_t k_tok_stride, int64_t v_tok_stride,
+                                   const int64_t *slot_mapping, int64_t ntok, int hkv,
+                                   int head_dim, int8_t *k_cache, float *k_scale,
+                                   uint8_t *v_cache, float *v_scale, float *v_zero,
+                                   int64_t num_pages, int64_t k_page_stride,
+                                   int64_t ks_page_stride, int64_t v_page_stride,
+                                   int64_t vs_page_stride, int64_t vz_page_stride, void *stream) {
+  using namespace k8v4;
+  clear_error();
+  K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)",
+               hkv);
+  K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)",
+               head_dim);
+  K8V4_REQUIRE(src_dtype == K8V4_F16 || src_dtype == K8V4_BF16, "k/v dtype must be fp16 or bf16");
+  K8V4_REQUIRE(ntok >= 0 && num_pages >= 0, "negative token or page count");
+  if (ntok == 0) return K8V4_OK;
+  K8V4_REQUIRE(k && v && slot_mapping && k_cache && k_scale && v_cache && v_scale && v_zero,
+               "null pointer");
+  K8V4_REQUIRE(k_tok_stride >= static_cast<int64_t>(hkv) * head_dim &&
+                   v_tok_stride >= static_cast<int64_t>(hkv) * head_dim,
+               "k/v token stride shorter than hkv*head_dim");
+  K8V4_REQUIRE(aligned(k_cache, 8) && aligned(v_cache, 4) && aligned(k_scale, 4) &&
+                   aligned(v_scale, 4) && aligned(v_zero, 4) && aligned(slot_mapping, 8),
+               "cache region or slot pointer misaligned");
+  K8V4_REQUIRE(k_page_stride % 8 == 0 && v_page_stride % 4 == 0 && ks_page_stride % 4 == 0 &&
+                   vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
+               "cache page strides must keep rows aligned");
+  K8V4_REQUIRE(aligned(k, 2) && aligned(v, 2), "k/v pointers misaligned");
+
+  StoreArgs a;
+  a.k = static_cast<const uint16_t *>(k);
+  a.v = static_cast<const uint16_t *>(v);
+  a.k_tok_stride = k_tok_stride;
+  a.v_tok_stride = v_tok_stride;
+  a.slots = slot_mapping;
+  a.units = ntok * hkv;
+  a.k_cache = k_cache;
+  a.k_scale = k_scale;
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.v_zero = v_zero;
+  a.num_pages = num_pages;
+  a.k_ps = k_page_stride;
+  a.ks_ps = ks_page_stride;
+  a.v_ps = v_page_stride;
+  a.vs_ps = vs_page_stride;
+  a.vz_ps = vz_page_stride;
+  a.hkv = hkv;
+  a.bf16 = src_dtype == K8V4_BF16;
+  a.vec_ok = aligned(k, 16) && aligned(v, 16) && (k_tok_stride % 8 == 0) && (v_tok_stride % 8 == 0);
+
+  const int upw = kWave / (head_dim / 8);
+  const int64_t waves = (a.units + upw - 1) / upw;
+  const int64_t blocks = (waves + 3) / 4;
+  K8V4_REQUIRE(blocks < (int64_t(1) << 31), "too many tokens for one launch");
+  auto s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    kv_store_kernel<128><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(a);
+  else
+    kv_store_kernel<256><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(a);
+  return launch_status("k8v4_kv_store_paged");
+}

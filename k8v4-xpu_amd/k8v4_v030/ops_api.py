@@ -1,0 +1,214 @@
+"""ctypes boundary into the gfx950 HIP library (``libk8v4_hip.so``).
+
+``ops()`` returns an object whose methods carry the names and argument orders
+of the reference's ``torch.ops.xe2_kv`` ops (k8v4_v030/ops_api.py:14-25,
+native/xe2_kv_ops.cpp:1779-1822), so callers written against the reference
+keep working.  Each method validates its tensors the way the reference's
+``TORCH_CHECK``s do (dtypes, ranks, within-page strides, the 2-or-4 head
+rule, with the same messages) and then passes raw device pointers, sizes and
+the current HIP stream to the C ABI declared in ``include/k8v4_abi.h``.
+Errors come back as ``RuntimeError``.  There is no fallback: a missing
+library raises ``FileNotFoundError`` and a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+from .layout import GQA, PAGE
+
+_DEFAULT_LIB = Path(__file__).resolve().parent / "libk8v4_hip.so"
+_LIB = None
+_LOADED: str | None = None
+_OPS = None
+
+F16, BF16, F32 = 0, 1, 2
+_DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_vp = ctypes.c_void_p
+
+
+def library_path() -> str:
+    """``K8V4_HIP_LIB`` if set, else the in-tree build."""
+    return os.environ.get("K8V4_HIP_LIB", str(_DEFAULT_LIB))
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.k8v4_abi_version.restype = _i32
+    lib.k8v4_abi_version.argtypes = []
+    lib.k8v4_last_error.restype = ctypes.c_char_p
+    lib.k8v4_last_error.argtypes = []
+    lib.k8v4_kv_store_paged.restype = _i32
+    lib.k8v4_kv_store_paged.argtypes = [
+        _vp, _vp, _i32, _i64, _i64, _vp, _i64, _i32, _i32,
+        _vp, _vp, _vp, _vp, _vp,
+        _i64, _i64, _i64, _i64, _i64, _i64, _vp,
+    ]
+    for name, argtypes, restype in _EXTRA_SYMBOLS:
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+
+
+# Entry points added by later kernels register here: (name, argtypes, restype).
+_EXTRA_SYMBOLS: list[tuple[str, list, object]] = []
+
+
+def load_library():
+    """Load the shared library once per process (path from :func:`library_path`)."""
+    global _LIB, _LOADED
+    path = library_path()
+    if _LOADED != path:
+        if not os.path.isfile(path):
+            raise FileNotFoundError("K8/V4 library is not at %s" % path)
+        lib = ctypes.CDLL(path)
+        _declare(lib)
+        _LIB, _LOADED = lib, path
+    return _LIB
+
+
+def _check(rc: int, lib) -> None:
+    if rc != 0:
+        raise RuntimeError(lib.k8v4_last_error().decode("utf-8", "replace"))
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def _checked_hkv(hkv: int) -> int:
+    _require(hkv in (2, 4), "unsupported per-GPU KV head count %d (this library serves 2 or 4)" % hkv)
+    return hkv
+
+
+def _on_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        _require(t.is_cuda, "K8/V4 ops need GPU tensors, got a %s tensor" % t.device.type)
+        _require(t.device == dev, "K8/V4 op tensors are on different devices")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return int(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return int(t.data_ptr())
+
+
+def check_paged_k(k_cache: torch.Tensor, k_scale: torch.Tensor, hkv: int, head_dim: int) -> None:
+    """Shape and within-page stride rules of the K views (xe2_kv_ops.cpp:1333-1349)."""
+    _require(k_cache.dtype == torch.int8, "k_cache int8")
+    _require(k_scale.dtype == torch.float32, "k_scale float32")
+    _require(
+        k_cache.dim() == 4 and tuple(k_cache.shape[1:]) == (PAGE, hkv, head_dim),
+        "k_cache [num_blocks,64,%d,%d] NHD" % (hkv, head_dim),
+    )
+    _require(
+        k_scale.dim() == 3 and tuple(k_scale.shape) == (k_cache.shape[0], PAGE, hkv),
+        "k_scale [num_blocks,64,%d]" % hkv,
+    )
+    _require(k_cache.stride()[1:] == (hkv * head_dim, head_dim, 1), "k_cache within-page strides")
+    _require(k_scale.stride()[1:] == (hkv, 1), "k_scale within-page strides")
+
+
+def check_paged_v(v_cache, v_scale, v_zero, hkv: int, head_dim: int) -> None:
+    """Shape and within-page stride rules of the V views (xe2_kv_ops.cpp:1352-1370)."""
+    cols = head_dim // 2
+    _require(v_cache.dtype == torch.uint8, "v_cache uint8 packed int4")
+    _require(v_scale.dtype == torch.float32 and v_zero.dtype == torch.float32, "v scale/zero float32")
+    _require(
+        v_cache.dim() == 4 and tuple(v_cache.shape[1:]) == (PAGE, hkv, cols),
+        "v_cache [num_blocks,64,%d,%d] NHD packed" % (hkv, cols),
+    )
+    _require(v_scale.shape == v_zero.shape, "v_scale/v_zero shape")
+    _require(
+        v_scale.dim() == 3 and tuple(v_scale.shape) == (v_cache.shape[0], PAGE, hkv),
+        "v_scale [num_blocks,64,%d]" % hkv,
+    )
+    _require(v_cache.stride()[1:] == (hkv * cols, cols, 1), "v_cache within-page strides")
+    _require(v_scale.stride()[1:] == (hkv, 1), "v_scale within-page")
+    _require(v_zero.stride()[1:] == (hkv, 1), "v_zero within-page")
+
+
+def cache_args(k_cache, k_scale, v_cache, v_scale, v_zero) -> list[int]:
+    """Pointers and byte page strides of the five region views, in ABI order."""
+    return [
+        _ptr(k_cache), _ptr(k_scale), _ptr(v_cache), _ptr(v_scale), _ptr(v_zero),
+        int(k_cache.shape[0]),
+        int(k_cache.stride(0)),
+        int(k_scale.stride(0)) * 4,
+        int(v_cache.stride(0)),
+        int(v_scale.stride(0)) * 4,
+        int(v_zero.stride(0)) * 4,
+    ]
+
+
+def _src_rows(t: torch.Tensor, name: str, hkv: int, head_dim: int) -> int:
+    """Validate a ``[T, hkv, D]`` 16-bit source; returns its token stride in elements."""
+    _require(t.dtype in (torch.float16, torch.bfloat16), "%s must be float16 or bfloat16" % name)
+    _require(t.dim() == 3 and t.shape[2] == head_dim, "%s [T,HKV,%d]" % (name, head_dim))
+    _require(t.shape[1] == hkv, "%s heads" % name)
+    _require(t.stride(2) == 1 and t.stride(1) == head_dim, "%s head/dim strides must be (%d, 1)" % (name, head_dim))
+    return int(t.stride(0)) if t.shape[0] > 1 else hkv * head_dim
+
+
+class _Ops:
+    """Methods named after the reference's ``torch.ops.xe2_kv`` schemas."""
+
+    def __init__(self, lib):
+        self._lib = lib
+
+    # -- quantize-and-write ------------------------------------------------
+    def kv_store_paged(self, k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero):
+        """Quantize K/V ``[T, HKV, D]`` into the paged cache at ``slot_mapping`` (int64 ``[T]``)."""
+        _require(k_fp16.dim() == 3, "k_fp16 [T,HKV,D]")
+        head_dim = int(k_fp16.shape[2])
+        _require(head_dim in (128, 256), "k_fp16 [T,HKV,D] with D in (128, 256)")
+        _require(k_fp16.dtype == v_fp16.dtype, "k/v_fp16 dtypes differ")
+        _require(v_fp16.shape == k_fp16.shape, "v_fp16 must match k_fp16")
+        _require(slot_mapping.dtype == torch.int64, "slot_mapping int64")
+        _require(slot_mapping.is_contiguous(), "slot_mapping must be contiguous")
+        hkv = _checked_hkv(int(k_fp16.shape[1]))
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        _require(k_cache.shape[0] == v_cache.shape[0], "k/v num_blocks")
+        _require(slot_mapping.numel() == k_fp16.shape[0], "slot_mapping [T]")
+        ks = _src_rows(k_fp16, "k_fp16", hkv, head_dim)
+        vs = _src_rows(v_fp16, "v_fp16", hkv, head_dim)
+        ntok = int(k_fp16.shape[0])
+        if ntok == 0:
+            return
+        dev = _on_gpu(k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero)
+        rc = self._lib.k8v4_kv_store_paged(
+            _ptr(k_fp16), _ptr(v_fp16), _DTYPE_CODE[k_fp16.dtype], ks, vs,
+            _ptr(slot_mapping), ntok, hkv, head_dim,
+            *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
+            _stream(dev),
+        )
+        _check(rc, self._lib)
+
+    def k_store_paged(self, *args, **kwargs):
+        raise RuntimeError("k_store_paged: use kv_store_paged (K and V are written by one kernel)")
+
+    def v_store_paged(self, *args, **kwargs):
+        raise RuntimeError("v_store_paged: use kv_store_paged (K and V are written by one kernel)")
+
+
+def ops() -> _Ops:
+    """The op table, after loading the library named by :func:`library_path`."""
+    global _OPS
+    lib = load_library()
+    if _OPS is None or _OPS._lib is not lib:
+        _OPS = _Ops(lib)
+    return _OPS
+
+
+__all__ = ["GQA", "PAGE", "library_path", "load_library", "ops", "check_paged_k", "check_paged_v"]
