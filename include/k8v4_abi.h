@@ -63,6 +63,44 @@ int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype, int64_t k_t
                         int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
                         int64_t vz_page_stride, void *stream);
 
+/*
+ * Paged decode / MTP verify for a batch with one common query length
+ * (replaces torch.ops.xe2_kv.int8k_int4v_attn_batch,
+ * k8v4_v030/native/xe2_kv_ops.cpp:1728-1775, with its stage-1 kernel :629-845
+ * and stage-2 merge :1057-1220).
+ *
+ * q:   [batch*q_len, 6*hkv, head_dim] (K8V4_F16 or K8V4_BF16), head stride
+ *      head_dim, dim stride 1, token stride q_tok_stride elements (multiple
+ *      of 8, base 16-byte aligned).  Row b*q_len + j is query token j of
+ *      sequence b.  Each row is int8-quantized with the K rule in the kernel.
+ * block_table: int32 [batch][bt_stride], first table_width entries used;
+ *      entry e covers kernel pages e*pages_per_block .. +pages_per_block-1.
+ * seq_lens: int32 [batch] (device).  visible_lens: NULL or int32
+ *      [batch][vis_stride] with [0] = page-valid length and [1+j] = causal
+ *      end of token j; without it the end of token j is
+ *      seq_len - q_len + j + 1.  A row with no visible key outputs zeros.
+ * out: [batch*q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride.
+ * workspace: caller-owned device scratch (16-byte aligned) of
+ *      workspace_bytes; k8v4_attn_workspace_bytes() gives what a call needs.
+ * num_splits: split-K work-groups (0 = about one per CU).
+ * Requires 1 <= q_len and q_len*6 <= 64.
+ */
+int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                    const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                    const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                    int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                    int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                    int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                    const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
+                    int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                    void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
+
+/* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
+ * No counterpart in the reference (its caller sized [nprog, 64, D] fp32
+ * partials, k8v4_v030/scratch.py:34-45, which is always at least this). */
+int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width, int pages_per_block,
+                                  int q_len, int hkv, int head_dim, int num_splits);
+
 #ifdef __cplusplus
 }
 #endif

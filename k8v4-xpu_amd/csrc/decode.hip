@@ -1,0 +1,743 @@
+// Paged decode / MTP-verify attention over the int8-K / int4-V cache.
+//
+// Reference semantics: k8v4_v030/oracle.py:100-163 (int8-quantized Q, exact
+// integer QK dot, fp softmax, V dequantized as (nibble - zero) * scale) and
+// the batch op k8v4_v030/native/xe2_kv_ops.cpp:1728-1775 with its stage-1
+// masking (:657-791) and stage-2 merge guards (:1086-1166).
+//
+// MI355X design (not a translation of the reference's per-page stage 1 +
+// per-row stage 2):
+//  * One launch covers the whole batch.  The grid is a fixed number G of
+//    split-K work-groups (about one per CU); every work-group derives, from
+//    the device-resident lengths, the same balanced plan: all live pages of
+//    all sequences are cut into runs of P pages that never straddle a
+//    sequence, so a batch of 4 x 128K and a batch of {2K, 32K, 128K, 200K}
+//    both fill the chip.  No host read of the lengths: graph-capturable.
+//  * A work-group is one wave per KV head.  The wave keeps the 6*q_len query
+//    rows of its head (padded to 16-row tiles) as int8 MFMA operands, so each
+//    K/V byte is fetched from HBM once and used for every GQA row.
+//  * Per 32-token chunk: QK^T on v_mfma_i32_16x16x64_i8 computed transposed
+//    (tokens x rows) so the score tile lands in the A-operand layout of the
+//    P.V MFMA; online softmax in the exp2 domain with a lazy rescale (the
+//    running max only moves when a row's max grows by more than 2^8); V
+//    nibbles expanded in registers to fp16 with a byte-permute + magic-number
+//    trick ((1024 + nibble) - (1024 + zero)) * scale; P.V and the row sums on
+//    v_mfma_f32_16x16x32_f16 with fp32 accumulation.
+//  * K, V and the scale planes of the next PF chunks are in flight in
+//    registers while the current chunk is computed (one wave per SIMD).
+//  * Each split writes (m, l, unnormalized O) for its live rows only; a small
+//    merge kernel combines the splits of each output row.
+#include "k8v4_common.h"
+
+#include <cfloat>
+
+namespace k8v4 {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Lazy-rescale threshold (log2 units): probabilities stay <= 2^8 before the
+// running max is moved, far inside fp16 range.
+constexpr float kRescaleThreshold = 8.0f;
+
+struct DecodeArgs {
+  const uint16_t *q;
+  int64_t q_tok_stride;  // elements; head stride is head_dim
+  int q_bf16;
+  const int8_t *k_cache;
+  const float *k_scale;
+  const uint8_t *v_cache;
+  const float *v_scale;
+  const float *v_zero;
+  int64_t num_pages;
+  int64_t k_ps, ks_ps, v_ps, vs_ps, vz_ps;  // page strides, bytes
+  const int32_t *block_table;
+  int64_t bt_stride;  // elements between table rows
+  int table_width;
+  int ppb;
+  const int32_t *seq_lens;
+  const int32_t *visible;  // nullable, [batch][vis_stride]
+  int64_t vis_stride;
+  int batch;
+  int q_len;
+  int hkv;
+  float *ws;
+  int64_t split_floats;  // floats of one split's state
+  int grid;              // number of split work-groups (the plan's G)
+  int min_pages;
+  void *out;
+  int out_dtype;
+  int64_t out_tok_stride;  // elements
+};
+
+// ---------------------------------------------------------------- planning
+// Every work-group of both kernels evaluates the same plan from device data.
+
+__device__ __forceinline__ int seq_len0(const DecodeArgs &a, int b) {
+  return a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride] : a.seq_lens[b];
+}
+
+__device__ __forceinline__ int seq_pages(const DecodeArgs &a, int b) {
+  const int L0 = seq_len0(a, b);
+  if (L0 <= 0) return 0;
+  const int64_t cap = static_cast<int64_t>(a.table_width) * a.ppb;
+  const int64_t n = (static_cast<int64_t>(L0) + kPage - 1) / kPage;
+  return static_cast<int>(n < cap ? n : cap);
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, kWave);
+  return x;
+}
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = max(x, __shfl_xor(x, m, kWave));
+  return x;
+}
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d, kWave);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Pages per split for this batch (same value in every lane and work-group).
+__device__ int plan_pages_per_split(const DecodeArgs &a, int lane) {
+  int total = 0, maxn = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += kWave) {
+    const int b = b0 + lane;
+    const int n = b < a.batch ? seq_pages(a, b) : 0;
+    total += n;
+    maxn = max(maxn, n);
+  }
+  total = wave_sum(total);
+  maxn = wave_max(maxn);
+  int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
+  P = max(P, a.min_pages);
+  return max(P, 1);
+}
+
+// Split index range [first, first + count) of sequence b, or the sequence
+// owning split w.  Sequences take ceil(pages / P) consecutive splits.
+struct SplitRange {
+  int b;
+  int first;
+  int count;
+};
+
+__device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want_b, int want_w) {
+  SplitRange r{-1, 0, 0};
+  int base = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += kWave) {
+    const int b = b0 + lane;
+    const int n = b < a.batch ? seq_pages(a, b) : 0;
+    const int s = (n + P - 1) / P;
+    const int incl = wave_inclusive_scan(s, lane);
+    const int excl = base + incl - s;
+    bool hit;
+    if (want_b >= 0)
+      hit = b == want_b;
+    else
+      hit = (s > 0) && (want_w >= excl) && (want_w < excl + s);
+    const uint64_t mask = __ballot(hit);
+    if (mask) {
+      const int src = __builtin_ctzll(mask);
+      r.b = b0 + src;
+      r.first = __shfl(excl, src, kWave);
+      r.count = __shfl(s, src, kWave);
+      return r;
+    }
+    base += __shfl(incl, kWave - 1, kWave);
+  }
+  return r;
+}
+
+__device__ __forceinline__ int physical_page(const DecodeArgs &a, const int32_t *bt_row, int p) {
+  if (a.ppb <= 1) return bt_row[p];
+  return bt_row[p / a.ppb] * a.ppb + (p % a.ppb);
+}
+
+// ------------------------------------------------------------ split kernel
+
+template <int D, int HKV>
+struct Chunk {
+  static constexpr int KS = D / 64;   // 64-dim steps of the QK MFMA
+  static constexpr int DG = D / 128;  // 16-lane groups of 8-dim dwords in a V row
+  static constexpr int SF = HKV / 2;  // scale floats each lane fetches per plane
+  v4i k[2][KS];
+  uint32_t v[DG][8];
+  float sc[3][SF];
+  int valid;  // physical page in range (wave-uniform)
+};
+
+// Token (0..31 within the chunk) held in slot i of a lane of group g:
+// the two 16-token halves of the QK^T output tile.
+__device__ __forceinline__ int chunk_token(int g, int i) { return i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4); }
+
+template <int D, int HKV>
+__device__ __forceinline__ void load_chunk(const DecodeArgs &a, const int32_t *bt_row, int x, int h,
+                                           int n, int g, int lane, Chunk<D, HKV> &c) {
+  using C = Chunk<D, HKV>;
+  const int p = x >> 1, half = x & 1;
+  int phys = physical_page(a, bt_row, p);
+  c.valid = (phys >= 0 && phys < a.num_pages) ? 1 : 0;
+  if (!c.valid) phys = 0;
+  const int tok0 = 32 * half;
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps +
+                   static_cast<int64_t>(tok0) * HKV * D + h * D;
+#pragma unroll
+  for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+      c.k[ml][ks] = *reinterpret_cast<const v4i *>(kb + (16 * ml + n) * (HKV * D) + 64 * ks + 16 * g);
+  const int64_t sc_off = static_cast<int64_t>(tok0) * HKV * 4 + lane * C::SF * 4;
+  const char *planes[3] = {reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps,
+                           reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps,
+                           reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps};
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const float *src = reinterpret_cast<const float *>(planes[r] + sc_off);
+#pragma unroll
+    for (int f = 0; f < C::SF; ++f) c.sc[r][f] = src[f];
+  }
+  const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps +
+                   static_cast<int64_t>(tok0) * HKV * (D / 2) + h * (D / 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int dg = 0; dg < C::DG; ++dg)
+      c.v[dg][i] = *reinterpret_cast<const uint32_t *>(vb + chunk_token(g, i) * (HKV * (D / 2)) + 64 * dg + 4 * n);
+}
+
+__device__ __forceinline__ v2h pack_h2(float lo, float hi) {
+  return __builtin_convertvector((v2f){lo, hi}, v2h);
+}
+
+template <int D, int NT, int HKV, int PF>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV, 64 * HKV), amdgpu_waves_per_eu(1, 1)))
+void decode_split_kernel(DecodeArgs a) {
+  using C = Chunk<D, HKV>;
+  constexpr int KS = C::KS, DG = C::DG, SF = C::SF;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = threadIdx.x / kWave;
+  const int n = lane & 15, g = lane >> 4;
+
+  const int P = plan_pages_per_split(a, lane);
+  const SplitRange sr = plan_locate(a, P, lane, -1, static_cast<int>(blockIdx.x));
+  if (sr.b < 0) return;  // idle work-group (uniform)
+  const int b = sr.b;
+  const int npages = seq_pages(a, b);
+  const int L0 = seq_len0(a, b);
+  const int p0 = (static_cast<int>(blockIdx.x) - sr.first) * P;
+  const int p1 = min(npages, p0 + P);
+  const int x0 = 2 * p0;
+  const int x1 = min(2 * p1, (L0 + 31) / 32);
+  const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
+  const int rows = a.q_len * kGqa;
+
+  // Causal ends: row r (token j = r / 6) sees keys t < lim(r).
+  int min_end = L0;
+  for (int j = 0; j < a.q_len; ++j) {
+    const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
+    min_end = min(min_end, e);
+  }
+  int lim[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r = 16 * nt + n;
+    if (r < rows) {
+      const int j = r / kGqa;
+      const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
+      lim[nt] = min(e, L0);
+    } else {
+      lim[nt] = L0;
+    }
+  }
+
+  // Prefetch the first chunks before the fp64 Q quantization.
+  C buf[PF];
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+    if (x0 + s < x1) load_chunk<D, HKV>(a, bt_row, x0 + s, h, n, g, lane, buf[s]);
+
+  // Q rows of this head -> int8 B operands, quantized with the store's K rule
+  // in float64 (oracle.py:22-40 applied to each query row).
+  v4i qb[NT][KS];
+  float crow[NT];
+  {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int r = 16 * nt + n;
+      float x[KS][16];
+      if (r < rows) {
+        const int j = r / kGqa;
+        const int qh = h * kGqa + (r - j * kGqa);
+        const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
+                              static_cast<int64_t>(qh) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint4 w0 = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g);
+          const uint4 w1 = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g + 8);
+          const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[ks][2 * e] = half_bits_to_float(static_cast<uint16_t>(words[e] & 0xFFFFu), a.q_bf16);
+            x[ks][2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(words[e] >> 16), a.q_bf16);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) x[ks][e] = 0.f;
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      const double scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
+      const double inv = amax == 0.f ? 0.0 : 1.0 / scale;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const double y = static_cast<double>(x[ks][e]) * inv;
+          double qv = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
+          qv = fmin(fmax(qv, -127.0), 127.0);
+          w[e >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(qv)) & 0xFFu) << (8 * (e & 3));
+        }
+        qb[nt][ks] = (v4i){static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
+                           static_cast<int>(w[3])};
+      }
+      // score * log2(e) = dot * q_scale * k_scale * log2(e) / sqrt(D); kept > 0
+      // so masked (-inf) scores never meet a zero factor.
+      const double c = scale * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
+      crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+    }
+  }
+
+  v4f O[NT][DG][8];
+  v4f lsum[NT];
+  float m_run[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    lsum[nt] = (v4f){0.f, 0.f, 0.f, 0.f};
+    m_run[nt] = -INFINITY;
+#pragma unroll
+    for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) O[nt][dg][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  const v8h ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  // Scale-plane element for (token slot i, head h): lane 2*T + h/SF, register h%SF.
+  const int sc_reg = h % SF;
+  const int sc_lane_off = h / SF;
+
+  for (int xb = x0; xb < x1; xb += PF) {
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+      const int x = xb + s;
+      if (x < x1) {
+        C &c = buf[s];
+        if (c.valid) {
+          // ---- QK^T, transposed: S[ml][nt] lane (n,g) reg i = score(token 16*ml+4g+i, row 16*nt+n)
+          v4i S[2][NT];
+#pragma unroll
+          for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              v4i acc = {0, 0, 0, 0};
+#pragma unroll
+              for (int ks = 0; ks < KS; ++ks)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.k[ml][ks], qb[nt][ks], acc, 0, 0, 0);
+              S[ml][nt] = acc;
+            }
+          // ---- scale planes for this lane's 8 tokens
+          float ksv[8], vsv[8], vzv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int src = 2 * chunk_token(g, i) + sc_lane_off;
+            ksv[i] = __shfl(c.sc[0][sc_reg], src, kWave);
+            vsv[i] = __shfl(c.sc[1][sc_reg], src, kWave);
+            vzv[i] = __shfl(c.sc[2][sc_reg], src, kWave);
+          }
+          const int tbase = 32 * x;
+          const bool masked = tbase + 32 > min_end;
+          if (masked) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              if (tbase + chunk_token(g, i) >= L0) {  // unwritten tail: never read its planes
+                ksv[i] = 0.f;
+                vsv[i] = 0.f;
+                vzv[i] = 0.f;
+              }
+            }
+          }
+          // ---- scores, chunk max, lazy rescale
+          float t[2][NT][4];
+          float mc[NT];
+          bool grow = false;
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float v = static_cast<float>(S[ml][nt][i]) * ksv[4 * ml + i];
+                if (masked && tbase + 16 * ml + 4 * g + i >= lim[nt]) v = -INFINITY;
+                t[ml][nt][i] = v;
+                mx = fmaxf(mx, v);
+              }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            mc[nt] = mx * crow[nt];
+            grow |= mc[nt] > m_run[nt] + kRescaleThreshold;
+          }
+          if (__ballot(grow)) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const float mnew = fmaxf(m_run[nt], mc[nt]);
+              const float alpha = m_run[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nt] - mnew);
+              m_run[nt] = mnew;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float ai = __shfl(alpha, 4 * g + i, kWave);
+                lsum[nt][i] *= ai;
+#pragma unroll
+                for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+                  for (int j = 0; j < 8; ++j) O[nt][dg][j][i] *= ai;
+              }
+            }
+          }
+          // ---- P = exp2(score * c - m), packed fp16 in the PV A-operand layout
+          v8h PA[NT];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const float nm = -fmaxf(m_run[nt], -FLT_MAX);
+            float p[8];
+#pragma unroll
+            for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                p[4 * ml + i] = __builtin_amdgcn_exp2f(fmaf(t[ml][nt][i], crow[nt], nm));
+            const v2h p01 = pack_h2(p[0], p[1]), p23 = pack_h2(p[2], p[3]);
+            const v2h p45 = pack_h2(p[4], p[5]), p67 = pack_h2(p[6], p[7]);
+            PA[nt] = (v8h){p01[0], p01[1], p23[0], p23[1], p45[0], p45[1], p67[0], p67[1]};
+            lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], ones, lsum[nt], 0, 0, 0);
+          }
+          // ---- V: nibbles -> ((1024 + q) - (1024 + zero)) * scale in fp16, token pairs
+          v2h vsp[4], nzp[4];
+#pragma unroll
+          for (int qp = 0; qp < 4; ++qp) {
+            vsp[qp] = pack_h2(vsv[2 * qp], vsv[2 * qp + 1]);
+            nzp[qp] = pack_h2(-1024.f - vzv[2 * qp], -1024.f - vzv[2 * qp + 1]);
+          }
+#pragma unroll
+          for (int dg = 0; dg < DG; ++dg) {
+#pragma unroll
+            for (int byte = 0; byte < 4; ++byte) {
+              const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + byte) << 16) | static_cast<uint32_t>(byte);
+              v2h be[4], bo[4];
+#pragma unroll
+              for (int qp = 0; qp < 4; ++qp) {
+                const uint32_t xw = __builtin_amdgcn_perm(c.v[dg][2 * qp + 1], c.v[dg][2 * qp], sel);
+                const uint32_t ev = (xw & 0x000F000Fu) | 0x64006400u;
+                const uint32_t od = ((xw >> 4) & 0x000F000Fu) | 0x64006400u;
+                be[qp] = (__builtin_bit_cast(v2h, ev) + nzp[qp]) * vsp[qp];
+                bo[qp] = (__builtin_bit_cast(v2h, od) + nzp[qp]) * vsp[qp];
+              }
+              const v8h Be = {be[0][0], be[0][1], be[1][0], be[1][1], be[2][0], be[2][1], be[3][0], be[3][1]};
+              const v8h Bo = {bo[0][0], bo[0][1], bo[1][0], bo[1][1], bo[2][0], bo[2][1], bo[3][0], bo[3][1]};
+#pragma unroll
+              for (int nt = 0; nt < NT; ++nt) {
+                O[nt][dg][2 * byte] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Be, O[nt][dg][2 * byte], 0, 0, 0);
+                O[nt][dg][2 * byte + 1] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Bo, O[nt][dg][2 * byte + 1], 0, 0, 0);
+              }
+            }
+          }
+        }
+        if (x + PF < x1) load_chunk<D, HKV>(a, bt_row, x + PF, h, n, g, lane, buf[s]);
+      }
+    }
+  }
+
+  // ---- split state: O rows (lane rows 16nt+4g+i, dims dg*128+8n+j), m, l
+  float *base = a.ws + static_cast<int64_t>(blockIdx.x) * a.split_floats;
+  float *mbase = base + static_cast<int64_t>(HKV) * rows * D;
+  float *lbase = mbase + HKV * rows;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * nt + 4 * g + i;
+      if (r < rows) {
+#pragma unroll
+        for (int dg = 0; dg < DG; ++dg) {
+          float *dst = base + static_cast<int64_t>(h * rows + r) * D + dg * 128 + 8 * n;
+          *reinterpret_cast<v4f *>(dst) =
+              (v4f){O[nt][dg][0][i], O[nt][dg][1][i], O[nt][dg][2][i], O[nt][dg][3][i]};
+          *reinterpret_cast<v4f *>(dst + 4) =
+              (v4f){O[nt][dg][4][i], O[nt][dg][5][i], O[nt][dg][6][i], O[nt][dg][7][i]};
+        }
+        if (n == 0) lbase[h * rows + r] = lsum[nt][i];
+      }
+    }
+    const int r = 16 * nt + n;
+    if (g == 0 && r < rows) mbase[h * rows + r] = m_run[nt];
+  }
+}
+
+// ------------------------------------------------------------ merge kernel
+// One 256-thread work-group per output row (token, query head).  Wave w
+// folds splits w, w+4, ...; the four partial states are combined in LDS.
+
+__device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
+  if (dtype == K8V4_F32)
+    static_cast<float *>(out)[idx] = v;
+  else if (dtype == K8V4_BF16)
+    static_cast<__bf16 *>(out)[idx] = static_cast<__bf16>(v);
+  else
+    static_cast<_Float16 *>(out)[idx] = static_cast<_Float16>(v);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int PER = D / kWave;  // dims per lane
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int hq = kGqa * a.hkv;
+  const int row_id = blockIdx.x;
+  const int qh = row_id % hq;
+  const int tok = row_id / hq;  // b * q_len + j
+  const int j = tok % a.q_len;
+  const int b = tok / a.q_len;
+  const int h = qh / kGqa;
+  const int rows = a.q_len * kGqa;
+  const int r = j * kGqa + (qh - h * kGqa);
+
+  const int P = plan_pages_per_split(a, lane);
+  const SplitRange sr = plan_locate(a, P, lane, b, -1);
+  const int first = sr.first, count = sr.b < 0 ? 0 : sr.count;
+
+  const int64_t o_off = static_cast<int64_t>(h * rows + r) * D;
+  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D + h * rows + r;
+  const int64_t l_off = m_off + a.hkv * rows;
+
+  // Global max over the splits of this row.
+  float M = -INFINITY;
+  for (int s = lane; s < count; s += kWave) M = fmaxf(M, a.ws[(first + s) * a.split_floats + m_off]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m, kWave));
+
+  float acc[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) acc[e] = 0.f;
+  float lacc = 0.f;
+  if (M != -INFINITY) {
+    for (int s = wv; s < count; s += 4) {
+      const float *st = a.ws + static_cast<int64_t>(first + s) * a.split_floats;
+      const float ms = st[m_off];
+      if (ms == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ms - M);
+      lacc += w * st[l_off];
+      const float *o = st + o_off + lane * PER;
+      if constexpr (PER == 2) {
+        const v2f v = *reinterpret_cast<const v2f *>(o);
+        acc[0] += w * v[0];
+        acc[1] += w * v[1];
+      } else {
+        const v4f v = *reinterpret_cast<const v4f *>(o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += w * v[e];
+      }
+    }
+  }
+  __shared__ float red[4][D + 1];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) red[wv][lane * PER + e] = acc[e];
+  if (lane == 0) red[wv][D] = lacc;
+  __syncthreads();
+  if (wv != 0) return;
+  const float l = red[0][D] + red[1][D] + red[2][D] + red[3][D];
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane * PER + e;
+    const float v = (red[0][d] + red[1][d] + red[2][d] + red[3][d]) * inv;
+    store_out(a.out, a.out_dtype, ob + d, v);
+  }
+}
+
+// ------------------------------------------------------------ host side
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+constexpr int kPrefetch = 2;
+
+template <int D, int HKV>
+void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
+  const dim3 grid(a.grid), block(64 * HKV);
+  switch (nt) {
+    case 1: decode_split_kernel<D, 1, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
+    case 2: decode_split_kernel<D, 2, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
+    case 3: decode_split_kernel<D, 3, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
+    default: decode_split_kernel<D, 4, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
+  }
+}
+
+int64_t split_state_floats(int hkv, int q_len, int head_dim) {
+  return static_cast<int64_t>(hkv) * q_len * kGqa * (head_dim + 2);
+}
+
+// Split work-groups for one call: about one per CU (a work-group is one wave
+// per KV head at one wave per SIMD), never more than the pages, capped by
+// the workspace and by an explicit request.
+int64_t choose_grid(int64_t batch, int64_t table_width, int ppb, int hkv, int64_t ws_splits, int requested) {
+  int64_t g = requested > 0 ? requested : static_cast<int64_t>(device_cus()) * (4 / hkv);
+  const int64_t pages = batch * table_width * ppb;
+  if (g > pages) g = pages;
+  if (g > ws_splits) g = ws_splits;
+  if (g < batch) g = batch;
+  return g;
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width, int pages_per_block, int q_len,
+                                             int hkv, int head_dim, int num_splits) {
+  using namespace k8v4;
+  if (batch < 1 || table_width < 1 || pages_per_block < 1 || q_len < 1 || !supported_heads(hkv) ||
+      !supported_dim(head_dim))
+    return -1;
+  const int64_t g = choose_grid(batch, table_width, pages_per_block, hkv, INT64_MAX, num_splits);
+  return g * split_state_floats(hkv, q_len, head_dim) * 4;
+}
+
+extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                               const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                               const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                               int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                               int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                               int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                               const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
+                               int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                               void *workspace, int64_t workspace_bytes, int num_splits, void *stream) {
+  using namespace k8v4;
+  clear_error();
+  K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
+  K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)", head_dim);
+  K8V4_REQUIRE(q_len >= 1 && q_len * kGqa <= kPage, "q_len*GQA exceeds BM (q_len=%d)", q_len);
+  K8V4_REQUIRE(pages_per_block >= 1, "pages_per_block");
+  K8V4_REQUIRE(num_pages >= 1, "empty cache");
+  K8V4_REQUIRE(batch >= 1 && batch < (1 << 24), "empty batch");
+  K8V4_REQUIRE(table_width >= 1 && table_width * pages_per_block < (int64_t(1) << 30), "block_table width");
+  K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
+  K8V4_REQUIRE(out_dtype == K8V4_F16 || out_dtype == K8V4_BF16 || out_dtype == K8V4_F32,
+               "out dtype must be fp16, bf16 or fp32");
+  K8V4_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && v_zero && block_table && seq_lens && out &&
+                   workspace,
+               "null pointer");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
+               "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
+  K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+  K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim, "out token stride shorter than HQ*D");
+  K8V4_REQUIRE(bt_stride >= table_width, "block_table row stride shorter than its width");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && k_page_stride % 16 == 0,
+               "k_cache must keep 16-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(v_cache) % 4 == 0 && v_page_stride % 4 == 0,
+               "v_cache must keep 4-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_scale) % 8 == 0 && reinterpret_cast<uintptr_t>(v_scale) % 8 == 0 &&
+                   reinterpret_cast<uintptr_t>(v_zero) % 8 == 0 && ks_page_stride % 8 == 0 &&
+                   vs_page_stride % 8 == 0 && vz_page_stride % 8 == 0,
+               "scale planes must be 8-byte aligned");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  if (visible_lens) K8V4_REQUIRE(vis_stride >= 1 + q_len, "visible_lens [B, 1+q_len]");
+
+  const int64_t split_floats = split_state_floats(hkv, q_len, head_dim);
+  const int64_t ws_splits = workspace_bytes / (split_floats * 4);
+  const int64_t grid = choose_grid(batch, table_width, pages_per_block, hkv, ws_splits, num_splits);
+  if (grid > ws_splits) {
+    set_error("K8/V4 workspace holds %lld split states, the batch needs at least %lld (%lld bytes each)",
+              static_cast<long long>(ws_splits), static_cast<long long>(grid),
+              static_cast<long long>(split_floats * 4));
+    return K8V4_ERR_WORKSPACE;
+  }
+
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t *>(q);
+  a.q_tok_stride = q_tok_stride;
+  a.q_bf16 = q_dtype == K8V4_BF16;
+  a.k_cache = k_cache;
+  a.k_scale = k_scale;
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.v_zero = v_zero;
+  a.num_pages = num_pages;
+  a.k_ps = k_page_stride;
+  a.ks_ps = ks_page_stride;
+  a.v_ps = v_page_stride;
+  a.vs_ps = vs_page_stride;
+  a.vz_ps = vz_page_stride;
+  a.block_table = block_table;
+  a.bt_stride = bt_stride;
+  a.table_width = static_cast<int>(table_width);
+  a.ppb = pages_per_block;
+  a.seq_lens = seq_lens;
+  a.visible = visible_lens;
+  a.vis_stride = vis_stride;
+  a.batch = static_cast<int>(batch);
+  a.q_len = q_len;
+  a.hkv = hkv;
+  a.ws = static_cast<float *>(workspace);
+  a.split_floats = split_floats;
+  a.grid = static_cast<int>(grid);
+  a.min_pages = 1;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.out_tok_stride = out_tok_stride;
+
+  auto s = static_cast<hipStream_t>(stream);
+  const int nt = (q_len * kGqa + 15) / 16;
+  if (head_dim == 128) {
+    if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
+  } else {
+    if (hkv == 4) launch_split<256, 4>(a, nt, s); else launch_split<256, 2>(a, nt, s);
+  }
+  int rc = launch_status("k8v4_attn_batch split");
+  if (rc) return rc;
+  const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv));
+  if (head_dim == 128)
+    decode_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
+  else
+    decode_merge_kernel<256><<<mgrid, dim3(256), 0, s>>>(a);
+  return launch_status("k8v4_attn_batch merge");
+}

@@ -55,8 +55,17 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.restype = restype
 
 
-# Entry points added by later kernels register here: (name, argtypes, restype).
-_EXTRA_SYMBOLS: list[tuple[str, list, object]] = []
+# Entry points beyond the store: (name, argtypes, restype).
+_EXTRA_SYMBOLS: list[tuple[str, list, object]] = [
+    (
+        "k8v4_attn_batch",
+        [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+         _vp, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
+         _vp, _i32, _i64, _vp, _i64, _i32, _vp],
+        _i32,
+    ),
+    ("k8v4_attn_workspace_bytes", [_i64, _i64, _i32, _i32, _i32, _i32, _i32], _i64),
+]
 
 
 def load_library():
@@ -192,6 +201,73 @@ class _Ops:
             _ptr(slot_mapping), ntok, hkv, head_dim,
             *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
             _stream(dev),
+        )
+        _check(rc, self._lib)
+
+    # -- decode / MTP verify ----------------------------------------------
+    def attn_workspace_bytes(self, batch: int, table_width: int, pages_per_block: int, q_len: int,
+                             hkv: int, head_dim: int, num_splits: int = 0) -> int:
+        """Scratch bytes :meth:`int8k_int4v_attn_batch` needs for this shape."""
+        n = int(self._lib.k8v4_attn_workspace_bytes(batch, table_width, pages_per_block, q_len, hkv,
+                                                    head_dim, num_splits))
+        _require(n > 0, "bad shape for the decode workspace")
+        return n
+
+    def int8k_int4v_attn_batch(self, q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
+                               block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws,
+                               out, q_len, pages_per_block, num_splits: int = 0):
+        """One uniform-q_len decode batch (argument order of the reference op).
+
+        ``q8``, ``q_scale``, ``m_ws``, ``l_ws`` and ``merged_ws`` are accepted for
+        signature compatibility and left untouched: Q is quantized inside the
+        kernel and the split-K state lives in the bytes of ``partials_ws``.
+        ``visible_lens`` is None, an empty tensor (derive causal ends from
+        ``seq_lens``) or int32 ``[B, >= 1 + q_len]``.
+        """
+        del q8, q_scale, m_ws, l_ws, merged_ws
+        q_len = int(q_len)
+        pages_per_block = int(pages_per_block)
+        _require(pages_per_block >= 1, "pages_per_block")
+        _require(q_len > 0 and q_len * GQA <= PAGE, "q_len*GQA exceeds BM")
+        _require(q_fp16.dim() == 3, "q_fp16 [T,HQ,D]")
+        head_dim = int(q_fp16.shape[2])
+        _require(head_dim in (128, 256), "q_fp16 [T,HQ,D] with D in (128, 256)")
+        _require(q_fp16.shape[1] % GQA == 0, "q_fp16 heads must be a multiple of GQA=6")
+        hkv = _checked_hkv(int(q_fp16.shape[1]) // GQA)
+        _require(q_fp16.dtype in (torch.float16, torch.bfloat16), "q_fp16 must be float16 or bfloat16")
+        _require(q_fp16.stride(2) == 1 and q_fp16.stride(1) == head_dim, "q_fp16 head/dim strides")
+        _require(out.shape == q_fp16.shape, "out shape")
+        _require(out.dtype in (torch.float16, torch.bfloat16, torch.float32), "out float16, bfloat16 or float32")
+        _require(out.stride(2) == 1 and out.stride(1) == head_dim, "out head/dim strides")
+        _require(q_fp16.shape[0] % q_len == 0, "T must be B*q_len")
+        batch = int(q_fp16.shape[0]) // q_len
+        _require(batch >= 1, "empty batch")
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        _require(k_cache.shape[0] == v_cache.shape[0], "k/v num_blocks")
+        _require(block_table.dtype == torch.int32, "block_table int32")
+        _require(block_table.dim() == 2 and block_table.shape[0] == batch, "block_table [B, splits]")
+        _require(block_table.stride(1) == 1, "block_table rows must be contiguous")
+        _require(int(block_table.shape[1]) > 0, "block_table n_splits")
+        _require(seq_lens.dtype == torch.int32 and seq_lens.numel() >= batch, "seq_lens [B]")
+        _require(seq_lens.is_contiguous(), "seq_lens XPU contig (graph input)")
+        vis_ptr, vis_stride = 0, 0
+        if visible_lens is not None and visible_lens.numel() > 0:
+            _require(visible_lens.dtype == torch.int32, "visible_lens int32")
+            _require(visible_lens.dim() == 2 and visible_lens.shape[0] == batch
+                     and visible_lens.shape[1] >= q_len + 1, "visible_lens [B, 1+q_len]")
+            _require(visible_lens.stride(1) == 1, "visible_lens rows must be contiguous")
+            vis_ptr, vis_stride = _ptr(visible_lens), int(visible_lens.stride(0))
+        _require(partials_ws is not None and partials_ws.is_contiguous(), "partials_ws must be a contiguous buffer")
+        dev = _on_gpu(q_fp16, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens, out, partials_ws)
+        ws_bytes = int(partials_ws.numel()) * partials_ws.element_size()
+        rc = self._lib.k8v4_attn_batch(
+            _ptr(q_fp16), _DTYPE_CODE[q_fp16.dtype], int(q_fp16.stride(0)),
+            *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
+            _ptr(block_table), int(block_table.stride(0)), int(block_table.shape[1]), pages_per_block,
+            _ptr(seq_lens), vis_ptr, vis_stride, batch, q_len, hkv, head_dim,
+            _ptr(out), _DTYPE_CODE[out.dtype], int(out.stride(0)),
+            _ptr(partials_ws), ws_bytes, int(num_splits), _stream(dev),
         )
         _check(rc, self._lib)
 

@@ -81,7 +81,8 @@ def decode_attention(
         t = np.arange(n)
         for g in range(geom.hkv):
             heads = slice(g * GQA, (g + 1) * GQA)
-            dots = np.einsum("jhd,td->jht", qc[:, heads].astype(np.float64), kf[:, g])
+            qg = qc[:, heads].astype(np.float64).reshape(q_len * GQA, d)
+            dots = (qg @ kf[:, g].T).reshape(q_len, GQA, n)  # exact: |dot| < 2^22
             scores = dots * qs[:, heads, None] * ksd[None, None, :, g] * inv_sqrt
             limit = np.minimum(np.asarray(ends)[:, None], n)  # [q_len, 1]
             scores = np.where((t[None, :] < limit)[:, None, :], scores, -np.inf)
@@ -117,7 +118,7 @@ def prefill_attention(
     for g in range(geom.hkv):
         heads = slice(g * GQA, (g + 1) * GQA)
         qg = q[rows][:, heads]  # [R, 6, D]
-        scores = np.einsum("rhd,sd->rhs", qg, k[:, g]) * float(scale)
+        scores = (qg.reshape(-1, d) @ k[:, g].T).reshape(rows.size, GQA, seq_len) * float(scale)
         scores = np.where(allow[:, None, :], scores, -np.inf)
         out[:, heads] = _softmax_rows(scores) @ v[:, g]
     return out

@@ -1,0 +1,315 @@
+"""Paged decode / MTP-verify kernel vs the oracle (GPU).
+
+Mirrors the reference's XPU regression suite (k8v4_v030/tests/test_kernel_xpu.py):
+partial pages and dirty tails, prefix copy-on-write, MTP-7 == serial q=1,
+builtin == explicit visible lengths, the int16 length wrap, manager-block
+tables and padded tables, and an 8-sequence batch in permuted order -- plus
+direct oracle parity (max-abs 2e-3 / rel 1e-2) at the benchmark shapes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_cases import DEV, Cache, assert_close, decode, fill_sequence, max_abs, random_tables, seeded_normal
+from k8v4_v030.layout import PAGE, PageLayout, as_int16, block_byte_span, pages_per_block, visible_lens
+from oracle import attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(cache, q, table, seq_lens, q_len, ppb=1, visible=None):
+    return attention.decode_attention(q.float().cpu().numpy(), cache.blob(), cache.geom, table.numpy(),
+                                      seq_lens.numpy(), q_len, ppb,
+                                      None if visible is None else visible.numpy())
+
+
+@pytest.mark.parametrize("hkv,d,q_len", [(4, 128, 7), (4, 128, 1), (2, 128, 3), (4, 128, 10),
+                                         (2, 256, 7), (4, 256, 1), (2, 256, 2)])
+def test_decode_matches_oracle_small(gpu_ops, hkv, d, q_len):
+    print("decode small hkv=%d d=%d q=%d" % (hkv, d, q_len), flush=True)
+    lay = PageLayout(hkv, d)
+    gen = torch.Generator().manual_seed(100 + 10 * hkv + q_len + d)
+    lengths = [1, 63, 64, 65, 130, 700, 2000]
+    table = random_tables(gen, lengths, 64, width=40)
+    cache = Cache(64, lay)
+    for b, L in enumerate(lengths):
+        fill_sequence(gpu_ops, cache, gen, table[b], L)
+    seq = torch.tensor(lengths, dtype=torch.int32)
+    q = seeded_normal(gen, (len(lengths) * q_len, lay.hq, d))
+    got = decode(gpu_ops, cache, q, table, seq, q_len).float().cpu().numpy()
+    want = _oracle(cache, q, table, seq, q_len)
+    err = assert_close(got, want, what="small")
+    print("  max abs err %.2e" % err, flush=True)
+
+
+def test_decode_config1_exact_shape(gpu_ops):
+    """1 sequence, context 2,048, q=1, 24/4 heads, D=128, table = randperm(64)[:32]."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(1001)
+    table = torch.randperm(64, generator=gen)[:32].to(torch.int32).view(1, 32)
+    cache = Cache(64, lay)
+    fill_sequence(gpu_ops, cache, gen, table[0], 2048)
+    q = seeded_normal(gen, (1, 24, 128))
+    seq = torch.tensor([2048], dtype=torch.int32)
+    got = decode(gpu_ops, cache, q, table, seq, 1).float().cpu().numpy()
+    assert_close(got, _oracle(cache, q, table, seq, 1), what="config1")
+
+
+def test_decode_config3_mtp_verify(gpu_ops):
+    """4 sequences x 8,192 context, 7 query tokens, random non-contiguous tables."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(1003)
+    lengths = [8192] * 4
+    table = random_tables(gen, lengths, 1024)
+    cache = Cache(1024, lay)
+    for b, L in enumerate(lengths):
+        fill_sequence(gpu_ops, cache, gen, table[b], L)
+    q = seeded_normal(gen, (4 * 7, 24, 128))
+    seq = torch.tensor(lengths, dtype=torch.int32)
+    got = decode(gpu_ops, cache, q, table, seq, 7).float().cpu().numpy()
+    err = assert_close(got, _oracle(cache, q, table, seq, 7), what="config3")
+    print("config3 max abs err %.2e" % err, flush=True)
+
+
+def test_decode_config4_mixed_long_shared_prefix(gpu_ops):
+    """Contexts {2,048; 32,768; 131,072; 200,000}, q=7, first 1,024 pages shared."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(1004)
+    lengths = [2048, 32768, 131072, 200000]
+    pages = [(L + 63) // 64 for L in lengths]
+    shared = 1024
+    unique = shared + sum(max(0, p - shared) for p in pages)
+    perm = torch.randperm(unique, generator=gen).to(torch.int32)
+    table = torch.zeros((4, max(pages)), dtype=torch.int32)
+    cur = shared
+    for b, p in enumerate(pages):
+        table[b, : min(p, shared)] = perm[: min(p, shared)]
+        if p > shared:
+            table[b, shared:p] = perm[cur : cur + p - shared]
+            cur += p - shared
+    cache = Cache(unique, lay)
+    print("config4: filling %d pages" % unique, flush=True)
+    # The longest sequence writes the shared prefix once; the others reuse it.
+    order = sorted(range(4), key=lambda b: -lengths[b])
+    fill_sequence(gpu_ops, cache, gen, table[order[0]], lengths[order[0]])
+    for b in order[1:]:
+        if pages[b] > shared:
+            fill_sequence(gpu_ops, cache, gen, table[b], lengths[b], start=shared * 64)
+    q = seeded_normal(gen, (4 * 7, 24, 128))
+    seq = torch.tensor(lengths, dtype=torch.int32)
+    got = decode(gpu_ops, cache, q, table, seq, 7).float().cpu().numpy()
+    print("config4: oracle", flush=True)
+    err = assert_close(got, _oracle(cache, q, table, seq, 7), what="config4")
+    print("config4 max abs err %.2e" % err, flush=True)
+
+
+@pytest.mark.parametrize("hkv", [2, 4])
+def test_partial_pages_negative_slots_and_dirty_tail(gpu_ops, hkv):
+    lay = PageLayout(hkv, 128)
+    cache = Cache(4, lay)
+    gen = torch.Generator().manual_seed(7)
+    key = seeded_normal(gen, (130, hkv, 128)).to(DEV)
+    value = seeded_normal(gen, (130, hkv, 128)).to(DEV)
+    slots = torch.arange(130, dtype=torch.int64, device=DEV)
+    slots[1] = -1
+    cache.store(gpu_ops, key, value, slots)
+    assert int(cache.views["k"][0, 1].abs().sum()) == 0
+    table = torch.arange(4, dtype=torch.int32).view(1, 4)
+
+    def run(L):
+        q = key[L - 1 : L].repeat_interleave(6, dim=1)
+        return decode(gpu_ops, cache, q, table, torch.tensor([L]), 1)
+
+    for L in (63, 64, 65, 127, 129):
+        out = run(L)
+        assert torch.isfinite(out).all() and float(out.abs().max()) > 0
+        q = key[L - 1 : L].repeat_interleave(6, dim=1)
+        assert_close(out.float().cpu().numpy(), _oracle(cache, q.cpu(), table, torch.tensor([L]), 1), what="L=%d" % L)
+    before, seen = run(108), run(109)
+    huge = torch.full((1, hkv, 128), 50.0, dtype=torch.float16, device=DEV)
+    cache.store(gpu_ops, huge, huge, torch.tensor([108], dtype=torch.int64, device=DEV))
+    masked, included = run(108), run(109)
+    assert max_abs(masked, before) < 1e-4
+    assert max_abs(included, seen) > 1e-3
+
+
+def test_unwritten_tail_with_nan_planes_is_masked(gpu_ops):
+    """Rows past seq_len hold NaN scale planes; they must not reach the output."""
+    lay = PageLayout(4, 128)
+    cache = Cache(2, lay)
+    cache.raw.view(torch.uint8).fill_(0xFF)  # every float plane is NaN
+    gen = torch.Generator().manual_seed(8)
+    fill_sequence(gpu_ops, cache, gen, torch.tensor([0, 1]), 70)
+    q = seeded_normal(gen, (7, 24, 128))
+    table = torch.tensor([[0, 1]], dtype=torch.int32)
+    got = decode(gpu_ops, cache, q, table, torch.tensor([70]), 7)
+    assert torch.isfinite(got).all()
+    assert_close(got.float().cpu().numpy(), _oracle(cache, q, table, torch.tensor([70]), 7), what="nan tail")
+
+
+@pytest.mark.parametrize("hkv", [2, 4])
+def test_prefix_cow_matches_source_and_mutation_diverges(gpu_ops, hkv):
+    lay = PageLayout(hkv, 128)
+    block_size = 2112
+    ratio = pages_per_block(block_size)
+    cache = Cache(2 * ratio, lay)
+    gen = torch.Generator().manual_seed(2112)
+    ntok = 60
+    key = seeded_normal(gen, (ntok, hkv, 128)).to(DEV)
+    value = seeded_normal(gen, (ntok, hkv, 128)).to(DEV)
+    cache.store(gpu_ops, key, value, torch.arange(ratio * PAGE, ratio * PAGE + ntok, device=DEV))
+    q = key[-1:].repeat_interleave(6, dim=1)
+    seq = torch.tensor([ntok])
+    src_out = decode(gpu_ops, cache, q, torch.tensor([[1]]), seq, 1, ppb=ratio)
+    before = decode(gpu_ops, cache, q, torch.tensor([[0]]), seq, 1, ppb=ratio)
+    assert max_abs(src_out, before) > 1e-3
+    src, nbytes = block_byte_span(1, block_size, lay)
+    dst, _ = block_byte_span(0, block_size, lay)
+    cache.raw[dst : dst + nbytes].copy_(cache.raw[src : src + nbytes])
+    copied = decode(gpu_ops, cache, q, torch.tensor([[0]]), seq, 1, ppb=ratio)
+    assert max_abs(src_out, copied) == 0.0
+    cache.views["v_scale"][0, ntok - 1] *= 2.0
+    mutated = decode(gpu_ops, cache, q, torch.tensor([[0]]), seq, 1, ppb=ratio)
+    assert torch.isfinite(mutated).all() and max_abs(src_out, mutated) > 1e-3
+
+
+@pytest.mark.parametrize("seq_len", [59500, 70000])
+def test_mtp7_long_properties(gpu_ops, seq_len):
+    """MTP-7 == serial q=1, builtin == explicit lengths, int16 wrap differs,
+    manager-block tables and padded tables agree (test_kernel_xpu.py:431-536)."""
+    lay = PageLayout(4, 128)
+    q_len = 7
+    n_pages = (seq_len + 63) // 64
+    cache = Cache(n_pages, lay)
+    gen = torch.Generator().manual_seed(seq_len)
+    identity = torch.arange(n_pages, dtype=torch.int32).view(1, -1)
+    fill_sequence(gpu_ops, cache, gen, identity[0], seq_len)
+    q = seeded_normal(gen, (q_len, 24, 128))
+    seq = torch.tensor([seq_len])
+    parallel = decode(gpu_ops, cache, q, identity, seq, q_len)
+    assert torch.isfinite(parallel).all() and float(parallel.abs().max()) > 0
+    serial = torch.cat([decode(gpu_ops, cache, q[j : j + 1], identity, torch.tensor([seq_len - (q_len - 1 - j)]), 1)
+                        for j in range(q_len)])
+    assert max_abs(parallel, serial) < 1e-3
+    vis = torch.tensor(visible_lens(seq_len, q_len), dtype=torch.int32).view(1, -1)
+    assert max_abs(parallel, decode(gpu_ops, cache, q, identity, seq, q_len, visible=vis)) < 1e-3
+    wrapped = decode(gpu_ops, cache, q, identity, torch.tensor([as_int16(seq_len)]), q_len)
+    assert max_abs(parallel, wrapped) > 1e-2
+    ratio = 26
+    blocks = torch.arange(-(-n_pages // ratio), dtype=torch.int32).view(1, -1)
+    assert max_abs(parallel, decode(gpu_ops, cache, q, blocks, seq, q_len, ppb=ratio)) < 1e-3
+    wide = torch.cat([identity, torch.zeros(1, 4, dtype=torch.int32)], dim=1)
+    assert max_abs(parallel, decode(gpu_ops, cache, q, wide, seq, q_len)) < 1e-3
+    assert_close(parallel.float().cpu().numpy(), _oracle(cache, q, identity, seq, q_len), what="mtp %d" % seq_len)
+
+
+def test_batch_of_eight_matches_per_sequence(gpu_ops):
+    lay = PageLayout(4, 128)
+    q_len = 7
+    lengths = [70000, 128, 512, 4096, 20000, 40000, 35000, 23333]
+    order = [1, 2, 4, 0, 6, 3, 7, 5]
+    gen = torch.Generator().manual_seed(88)
+    pages = [(L + 63) // 64 for L in lengths]
+    cache = Cache(sum(pages), lay)
+    tables, queries, singles = [], [], []
+    off = 0
+    for b, L in enumerate(lengths):
+        row = torch.arange(off, off + pages[b], dtype=torch.int32)
+        off += pages[b]
+        fill_sequence(gpu_ops, cache, gen, row, L)
+        qb = seeded_normal(gen, (q_len, 24, 128))
+        singles.append(decode(gpu_ops, cache, qb, row.view(1, -1), torch.tensor([L]), q_len))
+        tables.append(row)
+        queries.append(qb)
+    width = max(pages)
+    bt = torch.zeros((8, width), dtype=torch.int32)
+    qcat = torch.empty((8 * q_len, 24, 128), dtype=torch.float16)
+    lens = []
+    for r, src in enumerate(order):
+        bt[r, : pages[src]] = tables[src]
+        qcat[r * q_len : (r + 1) * q_len] = queries[src]
+        lens.append(lengths[src])
+    batched = decode(gpu_ops, cache, qcat, bt, torch.tensor(lens), q_len)
+    for r, src in enumerate(order):
+        assert max_abs(batched[r * q_len : (r + 1) * q_len], singles[src]) < 1e-3, (r, lens[r])
+    assert_close(batched.float().cpu().numpy(), _oracle(cache, qcat, bt, torch.tensor(lens), q_len), what="batch8")
+
+
+def test_zero_length_rows_and_output_dtypes(gpu_ops):
+    lay = PageLayout(4, 128)
+    cache = Cache(8, lay)
+    gen = torch.Generator().manual_seed(12)
+    table = torch.tensor([[0, 1, 2], [3, 4, 5]], dtype=torch.int32)
+    fill_sequence(gpu_ops, cache, gen, table[1], 150)
+    q = seeded_normal(gen, (2 * 3, 24, 128))
+    seq = torch.tensor([0, 150])
+    out16 = decode(gpu_ops, cache, q, table, seq, 3)
+    assert bool((out16[:3] == 0).all())
+    want = _oracle(cache, q, table, seq, 3)
+    out32 = decode(gpu_ops, cache, q, table, seq, 3, out_dtype=torch.float32)
+    assert_close(out32.cpu().numpy(), want, what="fp32 out")
+    outbf = decode(gpu_ops, cache, q.to(torch.bfloat16), table, seq, 3, out_dtype=torch.bfloat16)
+    assert torch.isfinite(outbf).all()
+    # bf16 Q is quantized from its own (rounded) values: compare against that oracle.
+    want_bf = _oracle(cache, q.to(torch.bfloat16), table, seq, 3)
+    assert_close(outbf.float().cpu().numpy(), want_bf, atol=8e-3, rtol=2e-2, what="bf16 out")
+
+
+def test_split_count_does_not_change_the_answer(gpu_ops):
+    lay = PageLayout(4, 128)
+    cache = Cache(300, lay)
+    gen = torch.Generator().manual_seed(31)
+    table = random_tables(gen, [9000, 5000], 300)
+    for b, L in enumerate([9000, 5000]):
+        fill_sequence(gpu_ops, cache, gen, table[b], L)
+    q = seeded_normal(gen, (14, 24, 128))
+    seq = torch.tensor([9000, 5000])
+    outs = [decode(gpu_ops, cache, q, table, seq, 7, num_splits=s) for s in (2, 3, 17, 64, 0)]
+    for o in outs[1:]:
+        assert max_abs(o, outs[0]) < 1e-3
+
+
+def test_rejects_bad_heads_and_q_len(gpu_ops):
+    lay = PageLayout(2, 128)
+    cache = Cache(4, lay)
+    table = torch.arange(4, dtype=torch.int32).view(1, 4)
+    for hkv in (3, 8, 1):
+        q = torch.randn(1, 6 * hkv, 128, dtype=torch.float16)
+        with pytest.raises(RuntimeError, match=r"unsupported per-GPU KV head count %d \(this library serves 2 or 4\)" % hkv):
+            decode(gpu_ops, cache, q, table, torch.tensor([4]), 1)
+    q = torch.randn(11, 12, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="q_len"):
+        decode(gpu_ops, cache, q, table, torch.tensor([40]), 11)
+
+
+def test_graph_capture_replays_with_new_lengths(gpu_ops):
+    """The op is capturable: replays read the device-resident lengths each time."""
+    lay = PageLayout(4, 128)
+    cache = Cache(200, lay)
+    gen = torch.Generator().manual_seed(41)
+    table = random_tables(gen, [6000, 6000], 200).to(DEV)
+    for b in range(2):
+        fill_sequence(gpu_ops, cache, gen, table[b].cpu(), 6000)
+    q = seeded_normal(gen, (14, 24, 128)).to(DEV)
+    seq = torch.tensor([6000, 6000], dtype=torch.int32, device=DEV)
+    nbytes = gpu_ops.attn_workspace_bytes(2, table.shape[1], 1, 7, 4, 128)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=DEV)
+    out = torch.zeros(q.shape, dtype=torch.float16, device=DEV)
+    args = (q, None, None, *cache.region_args(), table, seq, None, ws, None, None, None, out, 7, 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gpu_ops.int8k_int4v_attn_batch(*args)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gpu_ops.int8k_int4v_attn_batch(*args)
+    for lens in ([6000, 6000], [100, 5999], [4097, 1], [6000, 64]):
+        seq.copy_(torch.tensor(lens, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = decode(gpu_ops, cache, q.cpu(), table.cpu(), torch.tensor(lens), 7)
+        assert max_abs(replayed, eager) == 0.0, lens
