@@ -122,7 +122,7 @@ __device__ int plan_pages_per_split(const DecodeArgs &a, int lane) {
   maxn = wave_max(maxn);
   int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
   P = max(P, a.min_pages);
-  return max(P, 1);
+  return __builtin_amdgcn_readfirstlane(max(P, 1));
 }
 
 // Split index range [first, first + count) of sequence b, or the sequence
@@ -150,9 +150,10 @@ __device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want
     const uint64_t mask = __ballot(hit);
     if (mask) {
       const int src = __builtin_ctzll(mask);
-      r.b = b0 + src;
-      r.first = __shfl(excl, src, kWave);
-      r.count = __shfl(s, src, kWave);
+      // The results are wave-uniform; readfirstlane keeps them in SGPRs.
+      r.b = __builtin_amdgcn_readfirstlane(b0 + src);
+      r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, src, kWave));
+      r.count = __builtin_amdgcn_readfirstlane(__shfl(s, src, kWave));
       return r;
     }
     base += __shfl(incl, kWave - 1, kWave);
@@ -160,79 +161,340 @@ __device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want
   return r;
 }
 
+// Block-table reads go through the constant address space: the table is
+// read-only for the kernel's lifetime, so a uniform lookup becomes a scalar
+// load and never waits on the vector-memory counter the LDS DMA uses.
+typedef const __attribute__((address_space(4))) int32_t *const_i32_ptr;
+
 __device__ __forceinline__ int physical_page(const DecodeArgs &a, const int32_t *bt_row, int p) {
-  if (a.ppb <= 1) return bt_row[p];
-  return bt_row[p / a.ppb] * a.ppb + (p % a.ppb);
+  const const_i32_ptr row = (const_i32_ptr)(bt_row);
+  if (a.ppb <= 1) return row[p];
+  return row[p / a.ppb] * a.ppb + (p % a.ppb);
 }
 
 // ------------------------------------------------------------ split kernel
+//
+// Work-group = NWH waves per KV head.  Wave (h, w) handles KV head h and the
+// chunks x0 + w, x0 + w + NWH, ... of the work-group's page run.  Each wave
+// owns a ring of R LDS slots; a slot receives one 32-token chunk of its head
+// (K codes, V nibble words, the three scale planes) through direct-to-LDS DMA
+// loads (global_load_lds), so the next R-1 chunks stream in without holding
+// registers.  The LDS image of each slot is laid out so every read the MFMA
+// operands need is a linear, conflict-free ds_read.
 
-template <int D, int HKV>
-struct Chunk {
-  static constexpr int KS = D / 64;   // 64-dim steps of the QK MFMA
-  static constexpr int DG = D / 128;  // 16-lane groups of 8-dim dwords in a V row
-  static constexpr int SF = HKV / 2;  // scale floats each lane fetches per plane
-  v4i k[2][KS];
-  uint32_t v[DG][8];
-  float sc[3][SF];
-  int valid;  // physical page in range (wave-uniform)
+typedef __attribute__((address_space(3))) char lds_t;
+
+template <int D>
+struct Slot {
+  static constexpr int KS = D / 64;     // 64-dim k-steps of the QK MFMA
+  static constexpr int DG = D / 128;    // 8-dim dword groups per lane in a V row
+  static constexpr int VROW = D / 2;    // bytes of one token's V row (one head)
+  static constexpr int K_OFF = 0;       // [2*KS][64 lanes][16 B]: A-operand fragments
+  static constexpr int V_OFF = 32 * D;  // [32 tokens][VROW]: V rows as stored
+  static constexpr int S_OFF = V_OFF + 32 * VROW;  // ks[32] | vs[32] | vz[32] | vz[32] floats
+  static constexpr int BYTES = S_OFF + 512;
+  static constexpr int NV = 32 * VROW / 1024;       // 16-byte DMAs for the V rows
+  static constexpr int NDMA = 2 * KS + NV + 2;      // DMA instructions per chunk
 };
 
-// Token (0..31 within the chunk) held in slot i of a lane of group g:
-// the two 16-token halves of the QK^T output tile.
+// Token (0..31 within the chunk) held in slot i of a lane of group g: the two
+// 16-token halves of the transposed QK^T output tile.
 __device__ __forceinline__ int chunk_token(int g, int i) { return i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4); }
 
+__device__ __forceinline__ void dma(const void *src, lds_t *dst, int bytes) {
+  if (bytes == 16)
+    __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 4, 0, 0);
+}
+
+// Per-lane byte offsets of one chunk's DMA sources (loop-invariant).
+struct LaneOffsets {
+  uint32_t k;  // K row n (+16*ml), bytes 16g.. of a 64-dim step
+  uint32_t v;  // V: token (lane*16)/VROW (+rows of later DMAs), 16-byte column
+  uint32_t s;  // scale plane cell of token (lane & 31)
+};
+
 template <int D, int HKV>
-__device__ __forceinline__ void load_chunk(const DecodeArgs &a, const int32_t *bt_row, int x, int h,
-                                           int n, int g, int lane, Chunk<D, HKV> &c) {
-  using C = Chunk<D, HKV>;
+__device__ __forceinline__ LaneOffsets lane_offsets(int h, int n, int g, int lane) {
+  constexpr int VROW = D / 2;
+  LaneOffsets o;
+  o.k = static_cast<uint32_t>(n * (HKV * D) + h * D + 16 * g);
+  o.v = static_cast<uint32_t>(((lane * 16) / VROW) * (HKV * VROW) + h * VROW + (lane * 16) % VROW);
+  o.s = static_cast<uint32_t>(((lane & 31) * HKV + h) * 4);
+  return o;
+}
+
+// Starts the DMA of chunk x (32 tokens of head h) into `slot`; returns whether
+// the chunk's page is a valid cache page.  An invalid page still issues its
+// loads (from page 0) so every chunk costs the same vmcnt.  K and V move in
+// 16-byte-per-lane DMAs from a wave-uniform base plus a 32-bit lane offset;
+// the scale planes of this head are gathered with two 4-byte DMAs (lanes
+// 0-31: k_scale then v_zero, lanes 32-63: v_scale then v_zero again).
+template <int D, int HKV>
+__device__ __forceinline__ int issue_chunk(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
+                                           int lane, lds_t *slot) {
+  using S = Slot<D>;
   const int p = x >> 1, half = x & 1;
   int phys = physical_page(a, bt_row, p);
-  c.valid = (phys >= 0 && phys < a.num_pages) ? 1 : 0;
-  if (!c.valid) phys = 0;
+  const int valid = (phys >= 0 && phys < a.num_pages) ? 1 : 0;
+  if (!valid) phys = 0;
   const int tok0 = 32 * half;
-  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps +
-                   static_cast<int64_t>(tok0) * HKV * D + h * D;
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + static_cast<int64_t>(tok0) * HKV * D;
 #pragma unroll
-  for (int ml = 0; ml < 2; ++ml)
+  for (int ml = 0; ml < 2; ++ml) {
+    const char *kbm = kb + ml * 16 * HKV * D;
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks)
-      c.k[ml][ks] = *reinterpret_cast<const v4i *>(kb + (16 * ml + n) * (HKV * D) + 64 * ks + 16 * g);
-  const int64_t sc_off = static_cast<int64_t>(tok0) * HKV * 4 + lane * C::SF * 4;
-  const char *planes[3] = {reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps,
-                           reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps,
-                           reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps};
-#pragma unroll
-  for (int r = 0; r < 3; ++r) {
-    const float *src = reinterpret_cast<const float *>(planes[r] + sc_off);
-#pragma unroll
-    for (int f = 0; f < C::SF; ++f) c.sc[r][f] = src[f];
+    for (int ks = 0; ks < S::KS; ++ks) dma(kbm + lo.k + 64 * ks, slot + S::K_OFF + (ml * S::KS + ks) * 1024, 16);
   }
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps +
-                   static_cast<int64_t>(tok0) * HKV * (D / 2) + h * (D / 2);
+                   static_cast<int64_t>(tok0) * HKV * S::VROW;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int dg = 0; dg < C::DG; ++dg)
-      c.v[dg][i] = *reinterpret_cast<const uint32_t *>(vb + chunk_token(g, i) * (HKV * (D / 2)) + 64 * dg + 4 * n);
+  for (int j = 0; j < S::NV; ++j)
+    dma(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, slot + S::V_OFF + j * 1024, 16);
+  const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4 + lo.s;
+  const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0;
+  const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0;
+  const char *vzp = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + plane0;
+  dma(lane < 32 ? ksp : vsp, slot + S::S_OFF, 4);
+  dma(vzp, slot + S::S_OFF + 256, 4);
+  return valid;
 }
+
+// Wait until at most `after` chunks' DMAs are still in flight.
+template <int NDMA>
+__device__ __forceinline__ void wait_chunks(int after) {
+  static_assert(2 * NDMA <= 63, "vmcnt holds at most 63 outstanding loads");
+  if (after >= 2)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+  else if (after == 1)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// (x & mask) | bits in one v_and_or_b32 (the compiler otherwise emits an AND
+// and an OR with literal operands).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+  return r;
+}
+constexpr uint32_t kNibMask = 0x000F000Fu;  // low nibble of each 16-bit half
+constexpr uint32_t kMagic = 0x64006400u;    // fp16 1024.0 in both halves
 
 __device__ __forceinline__ v2h pack_h2(float lo, float hi) {
   return __builtin_convertvector((v2f){lo, hi}, v2h);
 }
 
-template <int D, int NT, int HKV, int PF>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV, 64 * HKV), amdgpu_waves_per_eu(1, 1)))
+// max(x, x from lane^16) and max(x, x from lane^32) without LDS.
+__device__ __forceinline__ float xlane_max16_32(float x) {
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
+template <int D, int NT, bool QLDS>
+struct WaveState {
+  static constexpr int KS = D / 64, DG = D / 128;
+  v4i qb[QLDS ? 1 : NT][KS];  // int8 Q rows as B operands (in LDS when QLDS)
+  float crow[NT];   // q_scale * log2(e) / sqrt(D), > 0
+  int lim[NT];      // causal end of this lane's row (S layout)
+  float m_run[NT];  // running max, log2 domain (S layout)
+  v4f lsum[NT];     // row sums (O layout, rows 4g+i)
+  v4f O[NT][DG][8]; // unnormalized output (O layout)
+};
+
+template <int D, int NT, bool QLDS>
+__device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const lds_t *slot, const lds_t *qlds,
+                                              int tbase, int L0, int lane, int g, bool masked) {
+  using S = Slot<D>;
+  constexpr int KS = S::KS, DG = S::DG;
+  // ---- QK^T, transposed: S[ml][nt] lane (n,g) reg i = score(token 16*ml+4g+i, row 16*nt+n)
+  v4i kf[2][KS];
+#pragma unroll
+  for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ml][ks] = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
+          slot + S::K_OFF + (ml * KS + ks) * 1024 + lane * 16);
+  v4i sc[2][NT];
+#pragma unroll
+  for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      v4i acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        v4i qf;
+        if constexpr (QLDS)
+          qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
+        else
+          qf = st.qb[nt][ks];
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, acc, 0, 0, 0);
+      }
+      sc[ml][nt] = acc;
+    }
+  // Phase fences keep the scheduler from hoisting later LDS reads into this
+  // phase, which would raise register pressure past two waves per SIMD.
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- scale planes of this lane's 8 tokens: [0..3] = tokens 4g+i, [4..7] = 16+4g+i
+  typedef float v4f_l __attribute__((ext_vector_type(4)));
+  const auto *sp = reinterpret_cast<const __attribute__((address_space(3))) v4f_l *>(slot + S::S_OFF);
+  v4f_l ksa = sp[g], ksb = sp[4 + g], vsa = sp[8 + g], vsb = sp[12 + g], vza = sp[16 + g], vzb = sp[20 + g];
+  float ksv[8] = {ksa[0], ksa[1], ksa[2], ksa[3], ksb[0], ksb[1], ksb[2], ksb[3]};
+  float vsv[8] = {vsa[0], vsa[1], vsa[2], vsa[3], vsb[0], vsb[1], vsb[2], vsb[3]};
+  float vzv[8] = {vza[0], vza[1], vza[2], vza[3], vzb[0], vzb[1], vzb[2], vzb[3]};
+  if (__builtin_expect(masked, 0)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (tbase + chunk_token(g, i) >= L0) {  // unwritten tail: never use its planes
+        ksv[i] = 0.f;
+        vsv[i] = 0.f;
+        vzv[i] = 0.f;
+      }
+    }
+  }
+  // ---- scores, chunk max, lazy rescale
+  float t[2][NT][4];
+  float mc[NT];
+  bool grow = false;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = static_cast<float>(sc[ml][nt][i]) * ksv[4 * ml + i];
+        t[ml][nt][i] = v;
+      }
+    if (__builtin_expect(masked, 0)) {
+#pragma unroll
+      for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tbase + 16 * ml + 4 * g + i >= st.lim[nt]) t[ml][nt][i] = -INFINITY;
+    }
+#pragma unroll
+    for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, t[ml][nt][i]);
+    mc[nt] = xlane_max16_32(mx) * st.crow[nt];
+    grow |= mc[nt] > st.m_run[nt] + kRescaleThreshold;
+  }
+  if (__ballot(grow)) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float mnew = fmaxf(st.m_run[nt], mc[nt]);
+      const float alpha = st.m_run[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m_run[nt] - mnew);
+      st.m_run[nt] = mnew;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ai = __shfl(alpha, 4 * g + i, kWave);
+        st.lsum[nt][i] *= ai;
+#pragma unroll
+        for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) st.O[nt][dg][j][i] *= ai;
+      }
+    }
+  }
+  // ---- P = exp2(score * c - m), packed fp16 in the PV A-operand layout; row sums by MFMA
+  const v8h ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  v8h PA[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float nm = -fmaxf(st.m_run[nt], -FLT_MAX);
+    float p[8];
+#pragma unroll
+    for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[4 * ml + i] = __builtin_amdgcn_exp2f(fmaf(t[ml][nt][i], st.crow[nt], nm));
+    const v2h p01 = pack_h2(p[0], p[1]), p23 = pack_h2(p[2], p[3]);
+    const v2h p45 = pack_h2(p[4], p[5]), p67 = pack_h2(p[6], p[7]);
+    PA[nt] = (v8h){p01[0], p01[1], p23[0], p23[1], p45[0], p45[1], p67[0], p67[1]};
+    st.lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], ones, st.lsum[nt], 0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- V: nibbles -> ((1024 + q) - (1024 + zero)) * scale in fp16, token pairs
+  v2h vsp[4], nzp[4];
+#pragma unroll
+  for (int qp = 0; qp < 4; ++qp) {
+    vsp[qp] = pack_h2(vsv[2 * qp], vsv[2 * qp + 1]);
+    nzp[qp] = pack_h2(-1024.f - vzv[2 * qp], -1024.f - vzv[2 * qp + 1]);
+  }
+#pragma unroll
+  for (int dg = 0; dg < DG; ++dg) {
+    uint32_t vw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      vw[i] = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+          slot + S::V_OFF + chunk_token(g, i) * S::VROW + 64 * dg + 4 * (lane & 15));
+#pragma unroll
+    for (int byte = 0; byte < 4; ++byte) {
+      const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + byte) << 16) | static_cast<uint32_t>(byte);
+      v2h be[4], bo[4];
+#pragma unroll
+      for (int qp = 0; qp < 4; ++qp) {
+        const uint32_t xw = __builtin_amdgcn_perm(vw[2 * qp + 1], vw[2 * qp], sel);
+        const uint32_t ev = and_or(xw, kNibMask, kMagic);
+        const uint32_t od = and_or(xw >> 4, kNibMask, kMagic);
+        be[qp] = (__builtin_bit_cast(v2h, ev) + nzp[qp]) * vsp[qp];
+        bo[qp] = (__builtin_bit_cast(v2h, od) + nzp[qp]) * vsp[qp];
+      }
+      const v8h Be = {be[0][0], be[0][1], be[1][0], be[1][1], be[2][0], be[2][1], be[3][0], be[3][1]};
+      const v8h Bo = {bo[0][0], bo[0][1], bo[1][0], bo[1][1], bo[2][0], bo[2][1], bo[3][0], bo[3][1]};
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        st.O[nt][dg][2 * byte] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Be, st.O[nt][dg][2 * byte], 0, 0, 0);
+        st.O[nt][dg][2 * byte + 1] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Bo, st.O[nt][dg][2 * byte + 1], 0, 0, 0);
+      }
+    }
+  }
+}
+
+template <int D, int NT, int HKV, int NWH>
+struct SplitConfig {
+  // Two waves per head keep the int8 Q operands in LDS (shared by the pair)
+  // and a 2-slot ring per wave; one wave per head keeps Q in registers and a
+  // 3-slot ring.
+  static constexpr bool QLDS = NWH > 1;
+  static constexpr int R = QLDS ? 2 : 3;  // LDS ring slots per wave
+  static constexpr int WAVES = HKV * NWH;
+  static constexpr int Q_BYTES_PER_HEAD = QLDS ? NT * (D / 64) * kWave * 16 : 0;
+  static constexpr int Q_OFF = WAVES * R * Slot<D>::BYTES;
+  static constexpr int RING_BYTES = Q_OFF + HKV * Q_BYTES_PER_HEAD;
+  // Partner-wave state exchange at the end (reuses the ring memory).
+  static constexpr int XCHG_FLOATS = (NT * (D / 128) * 8 * 4 + NT * 4 + NT) * kWave;
+  static constexpr int XCHG_BYTES = NWH > 1 ? HKV * XCHG_FLOATS * 4 : 0;
+  static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
+  static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
+};
+
+template <int D, int NT, int HKV, int NWH>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV * NWH, 64 * HKV * NWH),
+                          amdgpu_waves_per_eu(NWH, NWH)))
 void decode_split_kernel(DecodeArgs a) {
-  using C = Chunk<D, HKV>;
-  constexpr int KS = C::KS, DG = C::DG, SF = C::SF;
+  using S = Slot<D>;
+  using CFG = SplitConfig<D, NT, HKV, NWH>;
+  constexpr int KS = S::KS, DG = S::DG, R = CFG::R;
+  __shared__ __attribute__((aligned(16))) char lds_raw[CFG::LDS_BYTES];
+  lds_t *lds = (lds_t *)(lds_raw);
+
   const int lane = threadIdx.x & (kWave - 1);
-  const int h = threadIdx.x / kWave;
+  // Wave-uniform by construction; readfirstlane tells the compiler so, which
+  // keeps page lookups on the scalar unit.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int h = wave % HKV;   // KV head
+  const int w = wave / HKV;   // position among the NWH waves of this head
   const int n = lane & 15, g = lane >> 4;
 
   const int P = plan_pages_per_split(a, lane);
   const SplitRange sr = plan_locate(a, P, lane, -1, static_cast<int>(blockIdx.x));
-  if (sr.b < 0) return;  // idle work-group (uniform)
+  if (sr.b < 0) return;  // idle work-group (uniform over the work-group)
   const int b = sr.b;
   const int npages = seq_pages(a, b);
   const int L0 = seq_len0(a, b);
@@ -243,35 +505,38 @@ void decode_split_kernel(DecodeArgs a) {
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
 
+  // This wave's chunks: x0 + w + k*NWH for k < cnt.
+  const int my0 = x0 + w;
+  const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
+  lds_t *ring = lds + wave * R * S::BYTES;
+  const LaneOffsets lo = lane_offsets<D, HKV>(h, n, g, lane);
+  uint32_t valid_mask = 0;  // bit s: ring slot s holds a chunk of a valid page
+  for (int s = 0; s < R && s < cnt; ++s)
+    valid_mask |= static_cast<uint32_t>(issue_chunk<D, HKV>(a, bt_row, my0 + s * NWH, lo, lane, ring + s * S::BYTES)) << s;
+
+  WaveState<D, NT, CFG::QLDS> st;
+  lds_t *qlds = lds + CFG::Q_OFF + h * CFG::Q_BYTES_PER_HEAD;
   // Causal ends: row r (token j = r / 6) sees keys t < lim(r).
   int min_end = L0;
   for (int j = 0; j < a.q_len; ++j) {
     const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
     min_end = min(min_end, e);
   }
-  int lim[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int r = 16 * nt + n;
     if (r < rows) {
       const int j = r / kGqa;
       const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
-      lim[nt] = min(e, L0);
+      st.lim[nt] = min(e, L0);
     } else {
-      lim[nt] = L0;
+      st.lim[nt] = L0;
     }
   }
 
-  // Prefetch the first chunks before the fp64 Q quantization.
-  C buf[PF];
-#pragma unroll
-  for (int s = 0; s < PF; ++s)
-    if (x0 + s < x1) load_chunk<D, HKV>(a, bt_row, x0 + s, h, n, g, lane, buf[s]);
-
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
-  // in float64 (oracle.py:22-40 applied to each query row).
-  v4i qb[NT][KS];
-  float crow[NT];
+  // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
+  // both waves of the head quantize (they need crow) and wave 0 stores.
   {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -305,179 +570,112 @@ void decode_split_kernel(DecodeArgs a) {
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
-      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      amax = xlane_max16_32(amax);
       const double scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
       const double inv = amax == 0.f ? 0.0 : 1.0 / scale;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        uint32_t wq[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const double y = static_cast<double>(x[ks][e]) * inv;
           double qv = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
           qv = fmin(fmax(qv, -127.0), 127.0);
-          w[e >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(qv)) & 0xFFu) << (8 * (e & 3));
+          wq[e >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(qv)) & 0xFFu) << (8 * (e & 3));
         }
-        qb[nt][ks] = (v4i){static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
-                           static_cast<int>(w[3])};
+        const v4i frag = (v4i){static_cast<int>(wq[0]), static_cast<int>(wq[1]), static_cast<int>(wq[2]),
+                               static_cast<int>(wq[3])};
+        if constexpr (CFG::QLDS) {
+          if (w == 0)
+            *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16) = frag;
+        } else {
+          st.qb[nt][ks] = frag;
+        }
       }
       // score * log2(e) = dot * q_scale * k_scale * log2(e) / sqrt(D); kept > 0
       // so masked (-inf) scores never meet a zero factor.
       const double c = scale * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
-      crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+      st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
     }
   }
 
-  v4f O[NT][DG][8];
-  v4f lsum[NT];
-  float m_run[NT];
+  if constexpr (CFG::QLDS) __syncthreads();  // Q fragments visible to both waves of the head
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    lsum[nt] = (v4f){0.f, 0.f, 0.f, 0.f};
-    m_run[nt] = -INFINITY;
+    st.lsum[nt] = (v4f){0.f, 0.f, 0.f, 0.f};
+    st.m_run[nt] = -INFINITY;
 #pragma unroll
     for (int dg = 0; dg < DG; ++dg)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) O[nt][dg][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 8; ++j) st.O[nt][dg][j] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
-  const v8h ones = {1, 1, 1, 1, 1, 1, 1, 1};
-  // Scale-plane element for (token slot i, head h): lane 2*T + h/SF, register h%SF.
-  const int sc_reg = h % SF;
-  const int sc_lane_off = h / SF;
 
-  for (int xb = x0; xb < x1; xb += PF) {
-#pragma unroll
-    for (int s = 0; s < PF; ++s) {
-      const int x = xb + s;
-      if (x < x1) {
-        C &c = buf[s];
-        if (c.valid) {
-          // ---- QK^T, transposed: S[ml][nt] lane (n,g) reg i = score(token 16*ml+4g+i, row 16*nt+n)
-          v4i S[2][NT];
-#pragma unroll
-          for (int ml = 0; ml < 2; ++ml)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              v4i acc = {0, 0, 0, 0};
-#pragma unroll
-              for (int ks = 0; ks < KS; ++ks)
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(c.k[ml][ks], qb[nt][ks], acc, 0, 0, 0);
-              S[ml][nt] = acc;
-            }
-          // ---- scale planes for this lane's 8 tokens
-          float ksv[8], vsv[8], vzv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int src = 2 * chunk_token(g, i) + sc_lane_off;
-            ksv[i] = __shfl(c.sc[0][sc_reg], src, kWave);
-            vsv[i] = __shfl(c.sc[1][sc_reg], src, kWave);
-            vzv[i] = __shfl(c.sc[2][sc_reg], src, kWave);
-          }
-          const int tbase = 32 * x;
-          const bool masked = tbase + 32 > min_end;
-          if (masked) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              if (tbase + chunk_token(g, i) >= L0) {  // unwritten tail: never read its planes
-                ksv[i] = 0.f;
-                vsv[i] = 0.f;
-                vzv[i] = 0.f;
-              }
-            }
-          }
-          // ---- scores, chunk max, lazy rescale
-          float t[2][NT][4];
-          float mc[NT];
-          bool grow = false;
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int ml = 0; ml < 2; ++ml)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                float v = static_cast<float>(S[ml][nt][i]) * ksv[4 * ml + i];
-                if (masked && tbase + 16 * ml + 4 * g + i >= lim[nt]) v = -INFINITY;
-                t[ml][nt][i] = v;
-                mx = fmaxf(mx, v);
-              }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            mc[nt] = mx * crow[nt];
-            grow |= mc[nt] > m_run[nt] + kRescaleThreshold;
-          }
-          if (__ballot(grow)) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              const float mnew = fmaxf(m_run[nt], mc[nt]);
-              const float alpha = m_run[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nt] - mnew);
-              m_run[nt] = mnew;
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const float ai = __shfl(alpha, 4 * g + i, kWave);
-                lsum[nt][i] *= ai;
-#pragma unroll
-                for (int dg = 0; dg < DG; ++dg)
-#pragma unroll
-                  for (int j = 0; j < 8; ++j) O[nt][dg][j][i] *= ai;
-              }
-            }
-          }
-          // ---- P = exp2(score * c - m), packed fp16 in the PV A-operand layout
-          v8h PA[NT];
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            const float nm = -fmaxf(m_run[nt], -FLT_MAX);
-            float p[8];
-#pragma unroll
-            for (int ml = 0; ml < 2; ++ml)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                p[4 * ml + i] = __builtin_amdgcn_exp2f(fmaf(t[ml][nt][i], crow[nt], nm));
-            const v2h p01 = pack_h2(p[0], p[1]), p23 = pack_h2(p[2], p[3]);
-            const v2h p45 = pack_h2(p[4], p[5]), p67 = pack_h2(p[6], p[7]);
-            PA[nt] = (v8h){p01[0], p01[1], p23[0], p23[1], p45[0], p45[1], p67[0], p67[1]};
-            lsum[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], ones, lsum[nt], 0, 0, 0);
-          }
-          // ---- V: nibbles -> ((1024 + q) - (1024 + zero)) * scale in fp16, token pairs
-          v2h vsp[4], nzp[4];
-#pragma unroll
-          for (int qp = 0; qp < 4; ++qp) {
-            vsp[qp] = pack_h2(vsv[2 * qp], vsv[2 * qp + 1]);
-            nzp[qp] = pack_h2(-1024.f - vzv[2 * qp], -1024.f - vzv[2 * qp + 1]);
-          }
-#pragma unroll
-          for (int dg = 0; dg < DG; ++dg) {
-#pragma unroll
-            for (int byte = 0; byte < 4; ++byte) {
-              const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + byte) << 16) | static_cast<uint32_t>(byte);
-              v2h be[4], bo[4];
-#pragma unroll
-              for (int qp = 0; qp < 4; ++qp) {
-                const uint32_t xw = __builtin_amdgcn_perm(c.v[dg][2 * qp + 1], c.v[dg][2 * qp], sel);
-                const uint32_t ev = (xw & 0x000F000Fu) | 0x64006400u;
-                const uint32_t od = ((xw >> 4) & 0x000F000Fu) | 0x64006400u;
-                be[qp] = (__builtin_bit_cast(v2h, ev) + nzp[qp]) * vsp[qp];
-                bo[qp] = (__builtin_bit_cast(v2h, od) + nzp[qp]) * vsp[qp];
-              }
-              const v8h Be = {be[0][0], be[0][1], be[1][0], be[1][1], be[2][0], be[2][1], be[3][0], be[3][1]};
-              const v8h Bo = {bo[0][0], bo[0][1], bo[1][0], bo[1][1], bo[2][0], bo[2][1], bo[3][0], bo[3][1]};
-#pragma unroll
-              for (int nt = 0; nt < NT; ++nt) {
-                O[nt][dg][2 * byte] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Be, O[nt][dg][2 * byte], 0, 0, 0);
-                O[nt][dg][2 * byte + 1] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], Bo, O[nt][dg][2 * byte + 1], 0, 0, 0);
-              }
-            }
-          }
-        }
-        if (x + PF < x1) load_chunk<D, HKV>(a, bt_row, x + PF, h, n, g, lane, buf[s]);
-      }
+  for (int k = 0; k < cnt; ++k) {
+    const int s = k % R;  // wave-uniform ring slot
+    lds_t *slot = ring + s * S::BYTES;
+    wait_chunks<S::NDMA>(min(R - 1, cnt - 1 - k));
+    if ((valid_mask >> s) & 1u) {
+      const int tbase = 32 * (my0 + k * NWH);
+      compute_chunk<D, NT, CFG::QLDS>(st, slot, qlds, tbase, L0, lane, g, tbase + 32 > min_end);
+    }
+    if (k + R < cnt) {
+      // The slot's LDS reads above have completed (their values fed the MFMAs).
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint32_t v = static_cast<uint32_t>(issue_chunk<D, HKV>(a, bt_row, my0 + (k + R) * NWH, lo, lane, slot));
+      valid_mask = (valid_mask & ~(1u << s)) | (v << s);
     }
   }
 
-  // ---- split state: O rows (lane rows 16nt+4g+i, dims dg*128+8n+j), m, l
+  // ---- combine the NWH waves of each head, then write the split state
+  if constexpr (NWH > 1) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every ring is drained; reuse the LDS for the exchange
+    float *xb = reinterpret_cast<float *>(lds_raw) + h * (CFG::XCHG_FLOATS);
+    if (w == 1) {
+      int e = 0;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        xb[(e++) * kWave + lane] = st.m_run[nt];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xb[(e++) * kWave + lane] = st.lsum[nt][i];
+#pragma unroll
+        for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xb[(e++) * kWave + lane] = st.O[nt][dg][j][i];
+      }
+    }
+    __syncthreads();
+    if (w != 0) return;
+    int e = 0;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m1 = xb[(e++) * kWave + lane];
+      const float m0 = st.m_run[nt];
+      const float M = fmaxf(m0, m1);
+      const float a0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
+      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+      st.m_run[nt] = M;
+      float a0i[4], a1i[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a0i[i] = __shfl(a0, 4 * g + i, kWave);
+        a1i[i] = __shfl(a1, 4 * g + i, kWave);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.lsum[nt][i] = st.lsum[nt][i] * a0i[i] + xb[(e++) * kWave + lane] * a1i[i];
+#pragma unroll
+      for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            st.O[nt][dg][j][i] = st.O[nt][dg][j][i] * a0i[i] + xb[(e++) * kWave + lane] * a1i[i];
+    }
+  }
+
+  // Split state: O rows (lane rows 16nt+4g+i, dims dg*128+8n+j), m, l.
   float *base = a.ws + static_cast<int64_t>(blockIdx.x) * a.split_floats;
   float *mbase = base + static_cast<int64_t>(HKV) * rows * D;
   float *lbase = mbase + HKV * rows;
@@ -491,15 +689,15 @@ void decode_split_kernel(DecodeArgs a) {
         for (int dg = 0; dg < DG; ++dg) {
           float *dst = base + static_cast<int64_t>(h * rows + r) * D + dg * 128 + 8 * n;
           *reinterpret_cast<v4f *>(dst) =
-              (v4f){O[nt][dg][0][i], O[nt][dg][1][i], O[nt][dg][2][i], O[nt][dg][3][i]};
+              (v4f){st.O[nt][dg][0][i], st.O[nt][dg][1][i], st.O[nt][dg][2][i], st.O[nt][dg][3][i]};
           *reinterpret_cast<v4f *>(dst + 4) =
-              (v4f){O[nt][dg][4][i], O[nt][dg][5][i], O[nt][dg][6][i], O[nt][dg][7][i]};
+              (v4f){st.O[nt][dg][4][i], st.O[nt][dg][5][i], st.O[nt][dg][6][i], st.O[nt][dg][7][i]};
         }
-        if (n == 0) lbase[h * rows + r] = lsum[nt][i];
+        if (n == 0) lbase[h * rows + r] = st.lsum[nt][i];
       }
     }
     const int r = 16 * nt + n;
-    if (g == 0 && r < rows) mbase[h * rows + r] = m_run[nt];
+    if (g == 0 && r < rows) mbase[h * rows + r] = st.m_run[nt];
   }
 }
 
@@ -600,16 +798,19 @@ int device_cus() {
   return cached[dev];
 }
 
-constexpr int kPrefetch = 2;
+// Waves per KV head: two (two waves per SIMD) when the state fits 256
+// registers per wave, else one.
+template <int D, int NT>
+constexpr int waves_per_head() { return (D == 128 && NT <= 3) ? 2 : 1; }
 
 template <int D, int HKV>
 void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
-  const dim3 grid(a.grid), block(64 * HKV);
+  const dim3 grid(a.grid);
   switch (nt) {
-    case 1: decode_split_kernel<D, 1, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
-    case 2: decode_split_kernel<D, 2, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
-    case 3: decode_split_kernel<D, 3, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
-    default: decode_split_kernel<D, 4, HKV, kPrefetch><<<grid, block, 0, s>>>(a); break;
+    case 1: decode_split_kernel<D, 1, HKV, waves_per_head<D, 1>()><<<grid, dim3(64 * HKV * waves_per_head<D, 1>()), 0, s>>>(a); break;
+    case 2: decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a); break;
+    case 3: decode_split_kernel<D, 3, HKV, waves_per_head<D, 3>()><<<grid, dim3(64 * HKV * waves_per_head<D, 3>()), 0, s>>>(a); break;
+    default: decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a); break;
   }
 }
 
