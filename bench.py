@@ -1,0 +1,445 @@
+#!/usr/bin/env python3
+"""Benchmark of the k8v4 quantized paged-KV attention path on one MI355X.
+
+One step = one decode/MTP-verify layer call (split-K kernel + merge kernel)
+over the headline workload: 4 sequences x 131,072 cached tokens, 7 query
+tokens each, 24 Q / 4 KV heads, head_dim 128, 64-token pages, random
+non-contiguous block tables.  Prints ONE JSON line:
+
+* ``value``: whole-step throughput in GB/s of algorithmic KV bytes
+  (4 x 131,072 tokens x 816 B = 427,819,008 B per step), from the wall clock
+  around exactly ``--steps`` steps bracketed by device synchronisations;
+* ``roofline``: the split-K kernel alone, timed with HIP events recorded on
+  the stream it runs on (the library records one between its two kernels),
+  against the 8 TB/s HBM peak; ``traffic`` comes from the committed
+  rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
+* ``cpu_baseline``: the float64 oracle (oracle/attention.py) on one of the
+  four sequences, single-threaded, on this host;
+* ``configs``: microseconds per layer of the other workloads (store, short
+  decode, MTP verify, mixed long context, the D=256 per-rank shape).
+
+Inputs are synthetic: fp16 N(0,1) K/V quantized into the cache by the store
+kernel, fp16 N(0,1) queries.  Several copies of each cache are rotated from
+step to step so that no step finds its pages in the 256 MB MALL.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO / "k8v4-xpu_amd"), str(REPO)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "K8V4 paged-decode HBM GB/s (% of peak) + µs/layer at 4 seqs×128K ctx"
+TRAFFIC_PROFILE = REPO / "profiles" / "decode_split_kernel_headline_traffic.md"
+PAGE = 64
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--splits", type=int, default=0, help="split-K work-groups (0 = library default)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    return ap.parse_args(argv)
+
+
+# --------------------------------------------------------------------- HIP events
+class HipEvents:
+    """hipEvent_t helpers through the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise RuntimeError("the HIP runtime is not loaded")
+        self.lib = ctypes.CDLL(path)
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self) -> int:
+        ev = ctypes.c_void_p()
+        rc = self.lib.hipEventCreate(ctypes.byref(ev))
+        if rc != 0:
+            raise RuntimeError("hipEventCreate failed (%d)" % rc)
+        return ev.value
+
+    def record(self, ev: int, stream: int) -> None:
+        rc = self.lib.hipEventRecord(ctypes.c_void_p(ev), ctypes.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError("hipEventRecord failed (%d)" % rc)
+
+    def ms(self, a: int, b: int) -> float:
+        self.lib.hipEventSynchronize(ctypes.c_void_p(b))
+        out = ctypes.c_float()
+        rc = self.lib.hipEventElapsedTime(ctypes.byref(out), ctypes.c_void_p(a), ctypes.c_void_p(b))
+        if rc != 0:
+            raise RuntimeError("hipEventElapsedTime failed (%d)" % rc)
+        return float(out.value)
+
+    def destroy(self, ev: int) -> None:
+        self.lib.hipEventDestroy(ctypes.c_void_p(ev))
+
+
+# --------------------------------------------------------------------- workloads
+class DecodeWorkload:
+    """``copies`` independent caches of one decode shape in one page pool."""
+
+    def __init__(self, ops, torch, *, lengths, q_len, hkv, head_dim, copies, seed,
+                 pool_pages_per_copy=None, shared_prefix_pages=0, splits=0):
+        from k8v4_v030.layout import PageLayout
+        from k8v4_v030.cache_views import bind_regions
+
+        self.torch, self.ops = torch, ops
+        self.lengths = list(lengths)
+        self.batch = len(self.lengths)
+        self.q_len, self.hkv, self.head_dim = q_len, hkv, head_dim
+        self.layout = PageLayout(hkv, head_dim)
+        pages = [-(-n // PAGE) for n in self.lengths]
+        self.width = max(pages)
+        unique = shared_prefix_pages + sum(max(0, p - shared_prefix_pages) for p in pages)
+        per_copy = max(pool_pages_per_copy or 0, unique)
+        self.num_pages = per_copy * copies
+        gen = torch.Generator().manual_seed(seed)
+        self.raw = torch.empty(self.num_pages * self.layout.page_bytes, dtype=torch.int8, device="cuda")
+        self.views = bind_regions(self.raw, self.layout)
+        fill_pool(ops, torch, self.views, self.num_pages, hkv, head_dim, seed)
+        tables = []
+        for c in range(copies):
+            perm = torch.randperm(per_copy, generator=gen) + c * per_copy
+            table = torch.zeros((self.batch, self.width), dtype=torch.int32)
+            shared = perm[:shared_prefix_pages]
+            cur = shared_prefix_pages
+            for b, n in enumerate(pages):
+                s = min(n, shared_prefix_pages)
+                table[b, :s] = shared[:s].to(torch.int32)
+                table[b, s:n] = perm[cur : cur + n - s].to(torch.int32)
+                cur += n - s
+            tables.append(table.to("cuda"))
+        self.tables = tables
+        self.seq_lens = torch.tensor(self.lengths, dtype=torch.int32, device="cuda")
+        qgen = torch.Generator(device="cuda").manual_seed(seed + 1)
+        self.q = torch.randn((self.batch * q_len, 6 * hkv, head_dim), generator=qgen,
+                             dtype=torch.float16, device="cuda")
+        self.out = torch.empty_like(self.q)
+        nbytes = ops.attn_workspace_bytes(self.batch, self.width, 1, q_len, hkv, head_dim, splits)
+        self.ws = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+        self.splits = splits
+        self.kv_bytes = sum(self.lengths) * self.layout.bytes_per_token
+
+    def launch(self, i: int, split_done=None):
+        v = self.views
+        self.ops.int8k_int4v_attn_batch(
+            self.q, None, None, v["k"], v["k_scale"], v["v"], v["v_scale"], v["v_zero"],
+            self.tables[i % len(self.tables)], self.seq_lens, None, self.ws, None, None, None,
+            self.out, self.q_len, 1, num_splits=self.splits, split_done_event=split_done)
+
+
+def fill_pool(ops, torch, views, num_pages, hkv, head_dim, seed, chunk=65536):
+    """Every page of the pool gets quantized fp16 N(0,1) tokens from the store kernel."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    total = num_pages * PAGE
+    for s in range(0, total, chunk):
+        e = min(total, s + chunk)
+        k = torch.randn((e - s, hkv, head_dim), generator=gen, dtype=torch.float16, device="cuda")
+        v = torch.randn((e - s, hkv, head_dim), generator=gen, dtype=torch.float16, device="cuda")
+        slots = torch.arange(s, e, dtype=torch.int64, device="cuda")
+        ops.kv_store_paged(k, v, slots, views["k"], views["k_scale"], views["v"], views["v_scale"], views["v_zero"])
+
+
+class StoreWorkload:
+    """4 x 4,224 new tokens quantized into a 16,384-page cache (1% entries x20)."""
+
+    def __init__(self, ops, torch, *, copies, seed):
+        from k8v4_v030.layout import PageLayout
+        from k8v4_v030.cache_views import bind_regions
+
+        self.torch, self.ops = torch, ops
+        hkv, d, seqs, chunk = 4, 128, 4, 4224
+        self.layout = PageLayout(hkv, d)
+        self.num_pages = 16384
+        self.raw = torch.zeros(self.num_pages * self.layout.page_bytes, dtype=torch.int8, device="cuda")
+        self.views = bind_regions(self.raw, self.layout)
+        gen = torch.Generator().manual_seed(seed)
+        dgen = torch.Generator(device="cuda").manual_seed(seed)
+        ntok = seqs * chunk
+        self.inputs = []
+        for _ in range(copies):
+            kv = []
+            for _ in range(2):
+                x = torch.randn((ntok, hkv, d), generator=dgen, dtype=torch.float16, device="cuda")
+                hit = torch.rand(x.shape, generator=dgen, device="cuda") < 0.01
+                kv.append(torch.where(hit, x * 20, x))
+            pages = torch.randperm(self.num_pages, generator=gen)[: seqs * chunk // PAGE]
+            t = torch.arange(ntok)
+            slots = pages[t // PAGE] * PAGE + t % PAGE
+            self.inputs.append((kv[0], kv[1], slots.to("cuda")))
+        self.ntok = ntok
+        self.algo_bytes = ntok * hkv * d * 2 * 2 + ntok * 8 + ntok * self.layout.bytes_per_token
+
+    def launch(self, i: int, split_done=None):
+        k, v, slots = self.inputs[i % len(self.inputs)]
+        w = self.views
+        self.ops.kv_store_paged(k, v, slots, w["k"], w["k_scale"], w["v"], w["v_scale"], w["v_zero"])
+
+
+# --------------------------------------------------------------------- timing
+def progress(msg: str) -> None:
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def synchronize(torch):
+    if torch.distributed.is_available() and torch.distributed.is_initialized():
+        torch.distributed.barrier()
+    torch.cuda.synchronize()
+
+
+def timed_wall(torch, work, steps, warmup):
+    """Wall-clock seconds of exactly ``steps`` launches after ``warmup`` untimed ones."""
+    for i in range(warmup):
+        work.launch(i)
+    synchronize(torch)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        work.launch(warmup + i)
+    synchronize(torch)
+    return time.perf_counter() - t0
+
+
+def timed_events(torch, hip, work, steps, warmup, split_events=False):
+    """Per-launch GPU milliseconds from events on the launch stream.
+
+    Returns (step_ms, split_ms) lists; ``split_ms`` is empty unless the work
+    records a split-done event (decode only)."""
+    stream = int(torch.cuda.current_stream().cuda_stream)
+    for i in range(warmup):
+        work.launch(i)
+    synchronize(torch)
+    evs = [(hip.create(), hip.create(), hip.create()) for _ in range(steps)]
+    for i, (a, m, b) in enumerate(evs):
+        hip.record(a, stream)
+        work.launch(warmup + i, m if split_events else None)
+        hip.record(b, stream)
+    synchronize(torch)
+    step_ms = [hip.ms(a, b) for a, _, b in evs]
+    split_ms = [hip.ms(a, m) for a, m, _ in evs] if split_events else []
+    for e in evs:
+        for x in e:
+            hip.destroy(x)
+    return step_ms, split_ms
+
+
+def copy_peak_gbs(torch, hip, nbytes=1 << 30, reps=20):
+    """Read+write GB/s of a plain device copy (the calibration kernel for byte counters)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+
+    class _Copy:
+        def launch(self, i, split_done=None):
+            dst.copy_(src)
+
+    step_ms, _ = timed_events(torch, hip, _Copy(), reps, 3)
+    step_ms.sort()
+    return 2 * nbytes / (step_ms[len(step_ms) // 2] * 1e-3) / 1e9
+
+
+def traffic_from_profile():
+    """HBM bytes per split-kernel launch from the committed rocprofv3 PMC summary."""
+    if not TRAFFIC_PROFILE.is_file():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
+
+
+# --------------------------------------------------------------------- CPU baseline
+def cpu_baseline(torch, work, min_seconds=10.0, max_reps=5):
+    """The float64 oracle on the whole headline step (all sequences), one thread.
+
+    Repeats the step until ``min_seconds`` of CPU work (at most ``max_reps``)
+    and reports the median repetition; also returns the largest deviation of
+    the GPU output from the oracle on the same cache."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention, paged
+
+    work.launch(0)  # copy 0, whose table the oracle reads
+    torch.cuda.synchronize()
+    geom = paged.Geometry(work.hkv, work.head_dim)
+    raw_pages = work.raw.view(work.num_pages, work.layout.page_bytes)
+    seqs = []
+    for b, n in enumerate(work.lengths):
+        pages = -(-n // PAGE)
+        table = work.tables[0][b, :pages].long()
+        blob = raw_pages.index_select(0, table).view(torch.uint8).cpu().numpy().reshape(-1)
+        rows = slice(b * work.q_len, (b + 1) * work.q_len)
+        seqs.append((n, pages, blob, work.q[rows].cpu().numpy(), work.out[rows].double().cpu().numpy()))
+    reps, err = [], 0.0
+    with threadpool_limits(1):
+        while len(reps) < max_reps and (len(reps) < 1 or sum(reps) < min_seconds):
+            t0 = time.perf_counter()
+            outs = [attention.decode_attention(q, blob, geom, np.arange(pages)[None], [n], work.q_len)
+                    for n, pages, blob, q, _ in seqs]
+            reps.append(time.perf_counter() - t0)
+            err = max(float(np.abs(seqs[i][4] - outs[i]).max()) for i in range(len(seqs)))
+    sec = sorted(reps)[len(reps) // 2]
+    return {
+        "value": round(work.kv_bytes / sec / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "float64 numpy oracle (oracle/attention.py decode_attention) over the whole headline "
+                  "step: %d sequences x %d cached tokens, %d query tokens, 24 Q / 4 KV heads, D=128 "
+                  "(%d KV bytes); median of %d repetitions, 1 BLAS thread"
+                  % (work.batch, work.lengths[0], work.q_len, work.kv_bytes, len(reps)),
+        "seconds": round(sec, 3),
+        "gpu_vs_oracle_max_abs_err": err,
+    }
+
+
+# --------------------------------------------------------------------- configs
+def config_rows(torch, hip, ops, steps, warmup):
+    rows = {}
+
+    def decode_row(name, lengths, q_len, copies, seed, hkv=4, head_dim=128, **kw):
+        w = DecodeWorkload(ops, torch, lengths=lengths, q_len=q_len, hkv=hkv, head_dim=head_dim,
+                           copies=copies, seed=seed, **kw)
+        step_ms, split_ms = timed_events(torch, hip, w, steps, warmup, split_events=True)
+        us = 1e3 * sum(step_ms) / len(step_ms)
+        rows[name] = {
+            "us_per_layer": round(us, 2),
+            "us_per_layer_min": round(1e3 * min(step_ms), 2),
+            "split_kernel_us": round(1e3 * sum(split_ms) / len(split_ms), 2),
+            "kv_bytes": w.kv_bytes,
+            "GBps": round(w.kv_bytes / (us * 1e-6) / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * w.kv_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+            "cache_copies_rotated": copies,
+        }
+        del w
+        torch.cuda.empty_cache()
+        progress("%s: %.2f us/layer" % (name, us))
+
+    decode_row("1_decode_ctx2048_q1", [2048], 1, copies=128, seed=1001, pool_pages_per_copy=64)
+    w = StoreWorkload(ops, torch, copies=8, seed=1002)
+    step_ms, _ = timed_events(torch, hip, w, steps, warmup)
+    us = 1e3 * sum(step_ms) / len(step_ms)
+    rows["2_store_4x4224_tokens"] = {
+        "us_per_layer": round(us, 2),
+        "us_per_layer_min": round(1e3 * min(step_ms), 2),
+        "algorithmic_bytes": w.algo_bytes,
+        "GBps": round(w.algo_bytes / (us * 1e-6) / 1e9, 1),
+        "pct_of_hbm_peak": round(100 * w.algo_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+        "input_copies_rotated": 8,
+    }
+    progress("2_store_4x4224_tokens: %.2f us/layer" % us)
+    del w
+    torch.cuda.empty_cache()
+    decode_row("3_mtp_verify_4x8192_q7", [8192] * 4, 7, copies=12, seed=1003, pool_pages_per_copy=1024)
+    decode_row("4_mixed_long_q7", [2048, 32768, 131072, 200000], 7, copies=3, seed=1004,
+               shared_prefix_pages=1024)
+    rows["5_prefill_4224_over_131072"] = {"status": "not built"}
+    decode_row("reference_shape_d256_hkv2_ctx127853_q7", [127853], 7, copies=4, seed=1007,
+               hkv=2, head_dim=256)
+    return rows
+
+
+# --------------------------------------------------------------------- main
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(got --gpus %d)" % args.gpus, file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    from k8v4_v030.ops_api import ops
+
+    o = ops()
+    hip = HipEvents()
+    B, ctx, q_len = 4, 131072, 7
+    work = DecodeWorkload(o, torch, lengths=[ctx] * B, q_len=q_len, hkv=4, head_dim=128, copies=3,
+                          seed=1006, splits=args.splits)
+    progress("headline cache filled")
+    wall = timed_wall(torch, work, args.steps, args.warmup)
+    ms_per_step = 1e3 * wall / args.steps
+    gbs = work.kv_bytes / (wall / args.steps) / 1e9
+
+    step_ms, split_ms = timed_events(torch, hip, work, args.steps, args.warmup, split_events=True)
+    split_us = 1e3 * sum(split_ms) / len(split_ms)
+    merge_us = 1e3 * (sum(step_ms) - sum(split_ms)) / len(split_ms)
+    achieved = work.kv_bytes / (split_us * 1e-6) / 1e9
+    copy_gbs = copy_peak_gbs(torch, hip)
+    progress("headline: %.2f us/layer, split kernel %.2f us" % (1e3 * ms_per_step, split_us))
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8 QK (i32 acc) + f16 PV (f32 acc)",
+        "data": "synthetic",
+        "config": {
+            "workload": "paged decode / MTP verify: 4 seqs x 131072 cached tokens, 7 query tokens each, "
+                        "24 Q / 4 KV heads, head_dim 128, 64-token int8-K/int4-V pages, random block tables",
+            "batch": B, "context": ctx, "q_len": q_len, "hq": 24, "hkv": 4, "head_dim": 128,
+            "page_tokens": PAGE, "kv_bytes_per_step": work.kv_bytes, "cache_copies_rotated": 3,
+            "parallelism": "single GPU",
+        },
+        "us_per_layer": round(1e3 * ms_per_step, 2),
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "roofline": {
+            "kernel": "decode_split_kernel",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profile(),
+            "algorithmic_bytes_per_launch": work.kv_bytes,
+            "kernel_us": round(split_us, 2),
+            "merge_kernel_us": round(merge_us, 2),
+            "copy_peak_GBps": round(copy_gbs, 1),
+            "frac_of_copy_peak": round(achieved / copy_gbs, 4),
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, work)
+        progress("cpu baseline: %.1f s" % line["cpu_baseline"]["seconds"])
+    del work
+    torch.cuda.empty_cache()
+    if not args.no_configs:
+        line["configs"] = config_rows(torch, hip, o, min(args.steps, 100), min(args.warmup, 10))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -95,6 +95,25 @@ int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8
                     int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
                     void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
 
+/*
+ * k8v4_attn_batch plus one hipEvent_t (as void*, not NULL) recorded on
+ * `stream` between the split-K kernel and the merge kernel, so a caller can
+ * time each kernel with events on the stream it runs on.  No counterpart in
+ * the reference (its S1/S2 timing was an environment-driven log inside the
+ * op, xe2_kv_ops.cpp:1603-1621); results are identical to k8v4_attn_batch.
+ */
+int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
+                             const int8_t *k_cache, const float *k_scale, const uint8_t *v_cache,
+                             const float *v_scale, const float *v_zero, int64_t num_pages,
+                             int64_t k_page_stride, int64_t ks_page_stride, int64_t v_page_stride,
+                             int64_t vs_page_stride, int64_t vz_page_stride,
+                             const int32_t *block_table, int64_t bt_stride, int64_t table_width,
+                             int pages_per_block, const int32_t *seq_lens,
+                             const int32_t *visible_lens, int64_t vis_stride, int64_t batch,
+                             int q_len, int hkv, int head_dim, void *out, int out_dtype,
+                             int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
+                             int num_splits, void *stream, void *split_done_event);
+
 /* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
  * No counterpart in the reference (its caller sized [nprog, 64, D] fp32
  * partials, k8v4_v030/scratch.py:34-45, which is always at least this). */

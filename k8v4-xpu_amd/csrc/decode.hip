@@ -945,16 +945,17 @@ extern "C" int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width,
   return g * split_state_floats(hkv, q_len, head_dim) * 4;
 }
 
-extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
-                               const float *k_scale, const uint8_t *v_cache, const float *v_scale,
-                               const float *v_zero, int64_t num_pages, int64_t k_page_stride,
-                               int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
-                               int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
-                               int64_t table_width, int pages_per_block, const int32_t *seq_lens,
-                               const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
-                               int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
-                               void *workspace, int64_t workspace_bytes, int num_splits, void *stream) {
-  using namespace k8v4;
+namespace k8v4 {
+namespace {
+
+int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache, const float *k_scale,
+               const uint8_t *v_cache, const float *v_scale, const float *v_zero, int64_t num_pages,
+               int64_t k_page_stride, int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+               int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride, int64_t table_width,
+               int pages_per_block, const int32_t *seq_lens, const int32_t *visible_lens, int64_t vis_stride,
+               int64_t batch, int q_len, int hkv, int head_dim, void *out, int out_dtype,
+               int64_t out_tok_stride, void *workspace, int64_t workspace_bytes, int num_splits,
+               void *stream, hipEvent_t split_done) {
   clear_error();
   K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
   K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)", head_dim);
@@ -1037,10 +1038,57 @@ extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride,
   }
   int rc = launch_status("k8v4_attn_batch split");
   if (rc) return rc;
+  if (split_done) {
+    const hipError_t e = hipEventRecord(split_done, s);
+    if (e != hipSuccess) {
+      set_error("k8v4_attn_batch: hipEventRecord: %s", hipGetErrorString(e));
+      return K8V4_ERR_HIP;
+    }
+  }
   const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv));
   if (head_dim == 128)
     decode_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
   else
     decode_merge_kernel<256><<<mgrid, dim3(256), 0, s>>>(a);
   return launch_status("k8v4_attn_batch merge");
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                               const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                               const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                               int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                               int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                               int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                               const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
+                               int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                               void *workspace, int64_t workspace_bytes, int num_splits, void *stream) {
+  return k8v4::attn_batch(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
+                          k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                          block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
+                          vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
+                          workspace_bytes, num_splits, stream, nullptr);
+}
+
+extern "C" int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                                        const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                                        const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                                        int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                                        int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                                        int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                                        const int32_t *visible_lens, int64_t vis_stride, int64_t batch,
+                                        int q_len, int hkv, int head_dim, void *out, int out_dtype,
+                                        int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
+                                        int num_splits, void *stream, void *split_done_event) {
+  if (!split_done_event) {
+    k8v4::set_error("k8v4_attn_batch_profiled: null event");
+    return K8V4_ERR_ARG;
+  }
+  return k8v4::attn_batch(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
+                          k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                          block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
+                          vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
+                          workspace_bytes, num_splits, stream, static_cast<hipEvent_t>(split_done_event));
 }

@@ -66,6 +66,7 @@ _EXTRA_SYMBOLS: list[tuple[str, list, object]] = [
     ),
     ("k8v4_attn_workspace_bytes", [_i64, _i64, _i32, _i32, _i32, _i32, _i32], _i64),
 ]
+_EXTRA_SYMBOLS.append(("k8v4_attn_batch_profiled", _EXTRA_SYMBOLS[0][1] + [_vp], _i32))
 
 
 def load_library():
@@ -215,14 +216,16 @@ class _Ops:
 
     def int8k_int4v_attn_batch(self, q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
                                block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws,
-                               out, q_len, pages_per_block, num_splits: int = 0):
+                               out, q_len, pages_per_block, num_splits: int = 0, split_done_event=None):
         """One uniform-q_len decode batch (argument order of the reference op).
 
         ``q8``, ``q_scale``, ``m_ws``, ``l_ws`` and ``merged_ws`` are accepted for
         signature compatibility and left untouched: Q is quantized inside the
         kernel and the split-K state lives in the bytes of ``partials_ws``.
         ``visible_lens`` is None, an empty tensor (derive causal ends from
-        ``seq_lens``) or int32 ``[B, >= 1 + q_len]``.
+        ``seq_lens``) or int32 ``[B, >= 1 + q_len]``.  ``split_done_event``
+        (a raw hipEvent_t handle) is recorded between the split-K and merge
+        kernels, for timing them apart.
         """
         del q8, q_scale, m_ws, l_ws, merged_ws
         q_len = int(q_len)
@@ -261,14 +264,18 @@ class _Ops:
         _require(partials_ws is not None and partials_ws.is_contiguous(), "partials_ws must be a contiguous buffer")
         dev = _on_gpu(q_fp16, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens, out, partials_ws)
         ws_bytes = int(partials_ws.numel()) * partials_ws.element_size()
-        rc = self._lib.k8v4_attn_batch(
+        args = [
             _ptr(q_fp16), _DTYPE_CODE[q_fp16.dtype], int(q_fp16.stride(0)),
             *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
             _ptr(block_table), int(block_table.stride(0)), int(block_table.shape[1]), pages_per_block,
             _ptr(seq_lens), vis_ptr, vis_stride, batch, q_len, hkv, head_dim,
             _ptr(out), _DTYPE_CODE[out.dtype], int(out.stride(0)),
             _ptr(partials_ws), ws_bytes, int(num_splits), _stream(dev),
-        )
+        ]
+        if split_done_event is None:
+            rc = self._lib.k8v4_attn_batch(*args)
+        else:
+            rc = self._lib.k8v4_attn_batch_profiled(*args, int(split_done_event))
         _check(rc, self._lib)
 
     def k_store_paged(self, *args, **kwargs):
