@@ -143,13 +143,16 @@ class DecodeWorkload:
         self.ws = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
         self.splits = splits
         self.kv_bytes = sum(self.lengths) * self.layout.bytes_per_token
-
-    def launch(self, i: int, split_done=None):
         v = self.views
-        self.ops.int8k_int4v_attn_batch(
-            self.q, None, None, v["k"], v["k_scale"], v["v"], v["v_scale"], v["v_zero"],
-            self.tables[i % len(self.tables)], self.seq_lens, None, self.ws, None, None, None,
-            self.out, self.q_len, 1, num_splits=self.splits, split_done_event=split_done)
+        self.calls = [
+            ops.bind_int8k_int4v_attn_batch(
+                self.q, None, None, v["k"], v["k_scale"], v["v"], v["v_scale"], v["v_zero"], t,
+                self.seq_lens, None, self.ws, None, None, None, self.out, q_len, 1, num_splits=splits)
+            for t in self.tables
+        ]
+
+    def launch(self, i: int, split_done=None, stages=3):
+        self.calls[i % len(self.calls)](split_done_event=split_done, stages=stages)
 
 
 def fill_pool(ops, torch, views, num_pages, hkv, head_dim, seed, chunk=65536):
@@ -190,14 +193,14 @@ class StoreWorkload:
             pages = torch.randperm(self.num_pages, generator=gen)[: seqs * chunk // PAGE]
             t = torch.arange(ntok)
             slots = pages[t // PAGE] * PAGE + t % PAGE
-            self.inputs.append((kv[0], kv[1], slots.to("cuda")))
+            self.inputs.append(ops.bind_kv_store_paged(kv[0], kv[1], slots.to("cuda"), self.views["k"],
+                                                       self.views["k_scale"], self.views["v"],
+                                                       self.views["v_scale"], self.views["v_zero"]))
         self.ntok = ntok
         self.algo_bytes = ntok * hkv * d * 2 * 2 + ntok * 8 + ntok * self.layout.bytes_per_token
 
-    def launch(self, i: int, split_done=None):
-        k, v, slots = self.inputs[i % len(self.inputs)]
-        w = self.views
-        self.ops.kv_store_paged(k, v, slots, w["k"], w["k_scale"], w["v"], w["v_scale"], w["v_zero"])
+    def launch(self, i: int, split_done=None, stages=3):
+        self.inputs[i % len(self.inputs)]()
 
 
 # --------------------------------------------------------------------- timing
@@ -223,27 +226,22 @@ def timed_wall(torch, work, steps, warmup):
     return time.perf_counter() - t0
 
 
-def timed_events(torch, hip, work, steps, warmup, split_events=False):
-    """Per-launch GPU milliseconds from events on the launch stream.
-
-    Returns (step_ms, split_ms) lists; ``split_ms`` is empty unless the work
-    records a split-done event (decode only)."""
+def kernel_us(torch, hip, work, stages, steps, warmup):
+    """Average microseconds per launch of one decode stage, launched back to back
+    between two events on its stream (1 = split-K kernel, 2 = merge kernel)."""
     stream = int(torch.cuda.current_stream().cuda_stream)
     for i in range(warmup):
-        work.launch(i)
+        work.launch(i, stages=stages)
     synchronize(torch)
-    evs = [(hip.create(), hip.create(), hip.create()) for _ in range(steps)]
-    for i, (a, m, b) in enumerate(evs):
-        hip.record(a, stream)
-        work.launch(warmup + i, m if split_events else None)
-        hip.record(b, stream)
-    synchronize(torch)
-    step_ms = [hip.ms(a, b) for a, _, b in evs]
-    split_ms = [hip.ms(a, m) for a, m, _ in evs] if split_events else []
-    for e in evs:
-        for x in e:
-            hip.destroy(x)
-    return step_ms, split_ms
+    a, b = hip.create(), hip.create()
+    hip.record(a, stream)
+    for i in range(steps):
+        work.launch(warmup + i, stages=stages)
+    hip.record(b, stream)
+    us = 1e3 * hip.ms(a, b) / steps
+    hip.destroy(a)
+    hip.destroy(b)
+    return us
 
 
 def copy_peak_gbs(torch, hip, nbytes=1 << 30, reps=20):
@@ -252,12 +250,11 @@ def copy_peak_gbs(torch, hip, nbytes=1 << 30, reps=20):
     dst = torch.empty_like(src)
 
     class _Copy:
-        def launch(self, i, split_done=None):
+        def launch(self, i, split_done=None, stages=3):
             dst.copy_(src)
 
-    step_ms, _ = timed_events(torch, hip, _Copy(), reps, 3)
-    step_ms.sort()
-    return 2 * nbytes / (step_ms[len(step_ms) // 2] * 1e-3) / 1e9
+    us = kernel_us(torch, hip, _Copy(), 3, reps, 3)
+    return 2 * nbytes / (us * 1e-6) / 1e9
 
 
 def traffic_from_profile():
@@ -323,12 +320,11 @@ def config_rows(torch, hip, ops, steps, warmup):
     def decode_row(name, lengths, q_len, copies, seed, hkv=4, head_dim=128, **kw):
         w = DecodeWorkload(ops, torch, lengths=lengths, q_len=q_len, hkv=hkv, head_dim=head_dim,
                            copies=copies, seed=seed, **kw)
-        step_ms, split_ms = timed_events(torch, hip, w, steps, warmup, split_events=True)
-        us = 1e3 * sum(step_ms) / len(step_ms)
+        us = kernel_us(torch, hip, w, 3, steps, warmup)
         rows[name] = {
             "us_per_layer": round(us, 2),
-            "us_per_layer_min": round(1e3 * min(step_ms), 2),
-            "split_kernel_us": round(1e3 * sum(split_ms) / len(split_ms), 2),
+            "split_kernel_us": round(kernel_us(torch, hip, w, 1, steps, warmup), 2),
+            "merge_kernel_us": round(kernel_us(torch, hip, w, 2, steps, warmup), 2),
             "kv_bytes": w.kv_bytes,
             "GBps": round(w.kv_bytes / (us * 1e-6) / 1e9, 1),
             "pct_of_hbm_peak": round(100 * w.kv_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
@@ -340,11 +336,9 @@ def config_rows(torch, hip, ops, steps, warmup):
 
     decode_row("1_decode_ctx2048_q1", [2048], 1, copies=128, seed=1001, pool_pages_per_copy=64)
     w = StoreWorkload(ops, torch, copies=8, seed=1002)
-    step_ms, _ = timed_events(torch, hip, w, steps, warmup)
-    us = 1e3 * sum(step_ms) / len(step_ms)
+    us = kernel_us(torch, hip, w, 3, steps, warmup)
     rows["2_store_4x4224_tokens"] = {
         "us_per_layer": round(us, 2),
-        "us_per_layer_min": round(1e3 * min(step_ms), 2),
         "algorithmic_bytes": w.algo_bytes,
         "GBps": round(w.algo_bytes / (us * 1e-6) / 1e9, 1),
         "pct_of_hbm_peak": round(100 * w.algo_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
@@ -386,9 +380,8 @@ def main(argv=None) -> int:
     ms_per_step = 1e3 * wall / args.steps
     gbs = work.kv_bytes / (wall / args.steps) / 1e9
 
-    step_ms, split_ms = timed_events(torch, hip, work, args.steps, args.warmup, split_events=True)
-    split_us = 1e3 * sum(split_ms) / len(split_ms)
-    merge_us = 1e3 * (sum(step_ms) - sum(split_ms)) / len(split_ms)
+    split_us = kernel_us(torch, hip, work, 1, args.steps, args.warmup)
+    merge_us = kernel_us(torch, hip, work, 2, args.steps, args.warmup)
     achieved = work.kv_bytes / (split_us * 1e-6) / 1e9
     copy_gbs = copy_peak_gbs(torch, hip)
     progress("headline: %.2f us/layer, split kernel %.2f us" % (1e3 * ms_per_step, split_us))

@@ -96,11 +96,14 @@ int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8
                     void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
 
 /*
- * k8v4_attn_batch plus one hipEvent_t (as void*, not NULL) recorded on
- * `stream` between the split-K kernel and the merge kernel, so a caller can
- * time each kernel with events on the stream it runs on.  No counterpart in
- * the reference (its S1/S2 timing was an environment-driven log inside the
- * op, xe2_kv_ops.cpp:1603-1621); results are identical to k8v4_attn_batch.
+ * k8v4_attn_batch for timing its two kernels apart.  `split_done_event`
+ * (a hipEvent_t as void*, or NULL) is recorded on `stream` after the split-K
+ * kernel.  `stages` selects the kernels: 1 = split-K only (fills the
+ * workspace, leaves `out` untouched), 2 = merge only (reads the workspace a
+ * previous stages=1 call with the same arguments filled), 3 = both, which is
+ * exactly k8v4_attn_batch.  No counterpart in the reference (its S1/S2
+ * timing was an environment-driven host-synchronising log inside the op,
+ * k8v4_v030/native/xe2_kv_ops.cpp:1603-1621).
  */
 int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
                              const int8_t *k_cache, const float *k_scale, const uint8_t *v_cache,
@@ -112,7 +115,7 @@ int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
                              const int32_t *visible_lens, int64_t vis_stride, int64_t batch,
                              int q_len, int hkv, int head_dim, void *out, int out_dtype,
                              int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
-                             int num_splits, void *stream, void *split_done_event);
+                             int num_splits, void *stream, void *split_done_event, int stages);
 
 /* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
  * No counterpart in the reference (its caller sized [nprog, 64, D] fp32

@@ -955,8 +955,9 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
                int pages_per_block, const int32_t *seq_lens, const int32_t *visible_lens, int64_t vis_stride,
                int64_t batch, int q_len, int hkv, int head_dim, void *out, int out_dtype,
                int64_t out_tok_stride, void *workspace, int64_t workspace_bytes, int num_splits,
-               void *stream, hipEvent_t split_done) {
+               void *stream, hipEvent_t split_done, int stages) {
   clear_error();
+  K8V4_REQUIRE(stages >= 1 && stages <= 3, "stages must be 1 (split), 2 (merge) or 3 (both)");
   K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
   K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)", head_dim);
   K8V4_REQUIRE(q_len >= 1 && q_len * kGqa <= kPage, "q_len*GQA exceeds BM (q_len=%d)", q_len);
@@ -1031,13 +1032,15 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
 
   auto s = static_cast<hipStream_t>(stream);
   const int nt = (q_len * kGqa + 15) / 16;
-  if (head_dim == 128) {
-    if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
-  } else {
-    if (hkv == 4) launch_split<256, 4>(a, nt, s); else launch_split<256, 2>(a, nt, s);
+  if (stages & 1) {
+    if (head_dim == 128) {
+      if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
+    } else {
+      if (hkv == 4) launch_split<256, 4>(a, nt, s); else launch_split<256, 2>(a, nt, s);
+    }
+    const int rc = launch_status("k8v4_attn_batch split");
+    if (rc) return rc;
   }
-  int rc = launch_status("k8v4_attn_batch split");
-  if (rc) return rc;
   if (split_done) {
     const hipError_t e = hipEventRecord(split_done, s);
     if (e != hipSuccess) {
@@ -1045,6 +1048,7 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
       return K8V4_ERR_HIP;
     }
   }
+  if (!(stages & 2)) return K8V4_OK;
   const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv));
   if (head_dim == 128)
     decode_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
@@ -1069,7 +1073,7 @@ extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride,
                           k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
                           block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
                           vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
-                          workspace_bytes, num_splits, stream, nullptr);
+                          workspace_bytes, num_splits, stream, nullptr, 3);
 }
 
 extern "C" int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
@@ -1081,14 +1085,11 @@ extern "C" int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_to
                                         const int32_t *visible_lens, int64_t vis_stride, int64_t batch,
                                         int q_len, int hkv, int head_dim, void *out, int out_dtype,
                                         int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
-                                        int num_splits, void *stream, void *split_done_event) {
-  if (!split_done_event) {
-    k8v4::set_error("k8v4_attn_batch_profiled: null event");
-    return K8V4_ERR_ARG;
-  }
+                                        int num_splits, void *stream, void *split_done_event, int stages) {
   return k8v4::attn_batch(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
                           k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
                           block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
                           vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
-                          workspace_bytes, num_splits, stream, static_cast<hipEvent_t>(split_done_event));
+                          workspace_bytes, num_splits, stream, static_cast<hipEvent_t>(split_done_event),
+                          stages);
 }

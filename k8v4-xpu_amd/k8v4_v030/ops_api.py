@@ -66,7 +66,7 @@ _EXTRA_SYMBOLS: list[tuple[str, list, object]] = [
     ),
     ("k8v4_attn_workspace_bytes", [_i64, _i64, _i32, _i32, _i32, _i32, _i32], _i64),
 ]
-_EXTRA_SYMBOLS.append(("k8v4_attn_batch_profiled", _EXTRA_SYMBOLS[0][1] + [_vp], _i32))
+_EXTRA_SYMBOLS.append(("k8v4_attn_batch_profiled", _EXTRA_SYMBOLS[0][1] + [_vp, _i32], _i32))
 
 
 def load_library():
@@ -170,6 +170,29 @@ def _src_rows(t: torch.Tensor, name: str, hkv: int, head_dim: int) -> int:
     return int(t.stride(0)) if t.shape[0] > 1 else hkv * head_dim
 
 
+class BoundCall:
+    """One validated op call: the C entry point plus its argument list.
+
+    Calling it enqueues the op on the current stream of the call's device;
+    the tensors it was bound with are kept alive with it.
+    """
+
+    __slots__ = ("_lib", "_fn", "_profiled", "_args", "_dev", "_keep")
+
+    def __init__(self, lib, fn, args, dev, keep, profiled=None):
+        self._lib, self._fn, self._profiled = lib, fn, profiled
+        self._args, self._dev, self._keep = tuple(args), dev, keep
+
+    def __call__(self, split_done_event=None, stages: int = 3) -> None:
+        stream = _stream(self._dev)
+        if split_done_event is None and stages == 3:
+            rc = self._fn(*self._args, stream)
+        else:
+            _require(self._profiled is not None, "this op has no staged variant")
+            rc = self._profiled(*self._args, stream, int(split_done_event or 0), int(stages))
+        _check(rc, self._lib)
+
+
 class _Ops:
     """Methods named after the reference's ``torch.ops.xe2_kv`` schemas."""
 
@@ -179,6 +202,12 @@ class _Ops:
     # -- quantize-and-write ------------------------------------------------
     def kv_store_paged(self, k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero):
         """Quantize K/V ``[T, HKV, D]`` into the paged cache at ``slot_mapping`` (int64 ``[T]``)."""
+        bound = self.bind_kv_store_paged(k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero)
+        if bound is not None:
+            bound()
+
+    def bind_kv_store_paged(self, k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero):
+        """Validate a store once; returns a :class:`BoundCall` (None when there are no tokens)."""
         _require(k_fp16.dim() == 3, "k_fp16 [T,HKV,D]")
         head_dim = int(k_fp16.shape[2])
         _require(head_dim in (128, 256), "k_fp16 [T,HKV,D] with D in (128, 256)")
@@ -195,15 +224,15 @@ class _Ops:
         vs = _src_rows(v_fp16, "v_fp16", hkv, head_dim)
         ntok = int(k_fp16.shape[0])
         if ntok == 0:
-            return
-        dev = _on_gpu(k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero)
-        rc = self._lib.k8v4_kv_store_paged(
+            return None
+        tensors = (k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero)
+        dev = _on_gpu(*tensors)
+        args = [
             _ptr(k_fp16), _ptr(v_fp16), _DTYPE_CODE[k_fp16.dtype], ks, vs,
             _ptr(slot_mapping), ntok, hkv, head_dim,
             *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
-            _stream(dev),
-        )
-        _check(rc, self._lib)
+        ]
+        return BoundCall(self._lib, self._lib.k8v4_kv_store_paged, args, dev, tensors)
 
     # -- decode / MTP verify ----------------------------------------------
     def attn_workspace_bytes(self, batch: int, table_width: int, pages_per_block: int, q_len: int,
@@ -216,16 +245,36 @@ class _Ops:
 
     def int8k_int4v_attn_batch(self, q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
                                block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws,
-                               out, q_len, pages_per_block, num_splits: int = 0, split_done_event=None):
+                               out, q_len, pages_per_block, num_splits: int = 0, split_done_event=None,
+                               stages: int = 3):
         """One uniform-q_len decode batch (argument order of the reference op).
+
+        Validates and launches; :meth:`bind_int8k_int4v_attn_batch` takes the
+        same arguments and returns the validated call for repeated launches.
 
         ``q8``, ``q_scale``, ``m_ws``, ``l_ws`` and ``merged_ws`` are accepted for
         signature compatibility and left untouched: Q is quantized inside the
         kernel and the split-K state lives in the bytes of ``partials_ws``.
         ``visible_lens`` is None, an empty tensor (derive causal ends from
-        ``seq_lens``) or int32 ``[B, >= 1 + q_len]``.  ``split_done_event``
-        (a raw hipEvent_t handle) is recorded between the split-K and merge
-        kernels, for timing them apart.
+        ``seq_lens``) or int32 ``[B, >= 1 + q_len]``.
+
+        Timing hooks (no effect on results): ``split_done_event`` is a raw
+        hipEvent_t handle recorded after the split-K kernel; ``stages`` = 1 runs
+        only the split-K kernel, 2 only the merge (over the workspace a
+        ``stages=1`` call with the same arguments filled), 3 both.
+        """
+        self.bind_int8k_int4v_attn_batch(
+            q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens,
+            visible_lens, partials_ws, m_ws, l_ws, merged_ws, out, q_len, pages_per_block, num_splits,
+        )(split_done_event=split_done_event, stages=stages)
+
+    def bind_int8k_int4v_attn_batch(self, q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
+                                    block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws,
+                                    out, q_len, pages_per_block, num_splits: int = 0):
+        """Validate one decode call; returns a :class:`BoundCall` that launches it.
+
+        The call keeps the tensors' device addresses: their contents may change
+        between launches (new queries, lengths, tables), their storage may not.
         """
         del q8, q_scale, m_ws, l_ws, merged_ws
         q_len = int(q_len)
@@ -262,7 +311,8 @@ class _Ops:
             _require(visible_lens.stride(1) == 1, "visible_lens rows must be contiguous")
             vis_ptr, vis_stride = _ptr(visible_lens), int(visible_lens.stride(0))
         _require(partials_ws is not None and partials_ws.is_contiguous(), "partials_ws must be a contiguous buffer")
-        dev = _on_gpu(q_fp16, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens, out, partials_ws)
+        tensors = (q_fp16, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens, out, partials_ws)
+        dev = _on_gpu(*tensors)
         ws_bytes = int(partials_ws.numel()) * partials_ws.element_size()
         args = [
             _ptr(q_fp16), _DTYPE_CODE[q_fp16.dtype], int(q_fp16.stride(0)),
@@ -270,13 +320,11 @@ class _Ops:
             _ptr(block_table), int(block_table.stride(0)), int(block_table.shape[1]), pages_per_block,
             _ptr(seq_lens), vis_ptr, vis_stride, batch, q_len, hkv, head_dim,
             _ptr(out), _DTYPE_CODE[out.dtype], int(out.stride(0)),
-            _ptr(partials_ws), ws_bytes, int(num_splits), _stream(dev),
+            _ptr(partials_ws), ws_bytes, int(num_splits),
         ]
-        if split_done_event is None:
-            rc = self._lib.k8v4_attn_batch(*args)
-        else:
-            rc = self._lib.k8v4_attn_batch_profiled(*args, int(split_done_event))
-        _check(rc, self._lib)
+        keep = tensors + ((visible_lens,) if vis_ptr else ())
+        return BoundCall(self._lib, self._lib.k8v4_attn_batch, args, dev, keep,
+                         profiled=self._lib.k8v4_attn_batch_profiled)
 
     def k_store_paged(self, *args, **kwargs):
         raise RuntimeError("k_store_paged: use kv_store_paged (K and V are written by one kernel)")
@@ -294,4 +342,4 @@ def ops() -> _Ops:
     return _OPS
 
 
-__all__ = ["GQA", "PAGE", "library_path", "load_library", "ops", "check_paged_k", "check_paged_v"]
+__all__ = ["BoundCall", "GQA", "PAGE", "library_path", "load_library", "ops", "check_paged_k", "check_paged_v"]

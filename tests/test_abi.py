@@ -1,0 +1,107 @@
+"""The C ABI library without a GPU: it loads, exports every declared symbol with
+the argument count ops_api binds, and its host-side argument checks reject bad
+calls with the reference's messages before any device work is enqueued."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from k8v4_v030 import ops_api
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "k8v4_abi.h"
+
+
+def _declared() -> dict[str, int]:
+    """Function name -> parameter count, parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(k8v4_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = Path(ops_api.library_path())
+    if not path.is_file():
+        pytest.skip("library not built (run __graft_entry__.build())")
+    return ops_api.load_library()
+
+
+def test_header_declares_the_entry_points():
+    names = set(_declared())
+    assert {"k8v4_abi_version", "k8v4_last_error", "k8v4_kv_store_paged", "k8v4_attn_batch",
+            "k8v4_attn_batch_profiled", "k8v4_attn_workspace_bytes"} <= names
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    bound = {"k8v4_kv_store_paged": lib.k8v4_kv_store_paged.argtypes}
+    for name, argtypes, _ in ops_api._EXTRA_SYMBOLS:
+        bound[name] = argtypes
+    for name, nparams in _declared().items():
+        fn = getattr(lib, name)  # AttributeError if not exported
+        assert fn is not None
+        if name in bound:
+            assert len(bound[name]) == nparams, name
+    assert lib.k8v4_abi_version() == 1
+
+
+def _attn(lib, **over):
+    """k8v4_attn_batch with plausible host arguments and fake (never dereferenced) pointers."""
+    p = 0x10000
+    a = dict(q=p, q_dtype=0, q_tok_stride=24 * 128, k_cache=p, k_scale=p, v_cache=p, v_scale=p,
+             v_zero=p, num_pages=64, ks=52224, kss=52224, vs=52224, vss=52224, vzs=52224, bt=p,
+             bt_stride=32, width=32, ppb=1, seq=p, vis=None, vis_stride=0, batch=1, q_len=1, hkv=4,
+             d=128, out=p, out_dtype=0, out_stride=24 * 128, ws=p, ws_bytes=0, splits=0, stream=None)
+    a.update(over)
+    return lib.k8v4_attn_batch(*a.values())
+
+
+@pytest.mark.parametrize("hkv", [1, 3, 8])
+def test_attn_rejects_head_counts_with_the_reference_message(lib, hkv):
+    assert _attn(lib, hkv=hkv) == 1
+    msg = lib.k8v4_last_error().decode()
+    assert msg == "unsupported per-GPU KV head count %d (this library serves 2 or 4)" % hkv
+
+
+def test_attn_host_checks(lib):
+    assert _attn(lib, q_len=11) == 1 and "q_len*GQA exceeds BM" in lib.k8v4_last_error().decode()
+    assert _attn(lib, d=64) == 1 and "head dim" in lib.k8v4_last_error().decode()
+    assert _attn(lib, q=0x10008) == 1 and "16-byte" in lib.k8v4_last_error().decode()
+    assert _attn(lib, bt_stride=8) == 1 and "block_table" in lib.k8v4_last_error().decode()
+    assert _attn(lib, q_dtype=2) == 1 and "q dtype" in lib.k8v4_last_error().decode()
+    assert _attn(lib, ws=0) == 1 and "null" in lib.k8v4_last_error().decode()
+
+
+def test_store_rejects_head_counts(lib):
+    p = 0x10000
+    rc = lib.k8v4_kv_store_paged(p, p, 0, 3 * 128, 3 * 128, p, 10, 3, 128, p, p, p, p, p, 64,
+                                 52224, 52224, 52224, 52224, 52224, None)
+    assert rc == 1
+    assert "unsupported per-GPU KV head count 3" in lib.k8v4_last_error().decode()
+
+
+def test_workspace_bytes_rejects_bad_shapes(lib):
+    assert lib.k8v4_attn_workspace_bytes(0, 32, 1, 1, 4, 128, 0) == -1
+    assert lib.k8v4_attn_workspace_bytes(1, 32, 1, 1, 3, 128, 0) == -1
+    assert lib.k8v4_attn_workspace_bytes(1, 32, 1, 1, 4, 96, 0) == -1
+    # An explicit split count fixes the size: splits x hkv x q_len x 6 x (D + 2) x 4 bytes.
+    assert lib.k8v4_attn_workspace_bytes(4, 2048, 1, 7, 4, 128, 64) == 64 * 4 * 7 * 6 * 130 * 4
+
+
+def test_ops_layer_raises_without_gpu_tensors(lib):
+    import torch
+
+    from k8v4_v030.cache_views import bind_regions
+    from k8v4_v030.layout import PageLayout
+
+    lay = PageLayout(4, 128)
+    v = bind_regions(torch.zeros(2 * lay.page_bytes, dtype=torch.int8), lay)
+    k = torch.zeros(3, 4, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        ops_api.ops().kv_store_paged(k, k, torch.zeros(3, dtype=torch.int64), v["k"], v["k_scale"], v["v"],
+                                     v["v_scale"], v["v_zero"])

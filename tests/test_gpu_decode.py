@@ -313,3 +313,46 @@ def test_graph_capture_replays_with_new_lengths(gpu_ops):
         replayed = out.clone()
         eager = decode(gpu_ops, cache, q.cpu(), table.cpu(), torch.tensor(lens), 7)
         assert max_abs(replayed, eager) == 0.0, lens
+
+
+def test_bound_call_and_stages_match_the_plain_op(gpu_ops):
+    """bind_* launches the same kernels; stages 1 then 2 equal stages 3, bit for bit."""
+    lay = PageLayout(4, 128)
+    cache = Cache(300, lay)
+    gen = torch.Generator().manual_seed(53)
+    table = random_tables(gen, [9000, 3000], 300)
+    for b, L in enumerate([9000, 3000]):
+        fill_sequence(gpu_ops, cache, gen, table[b], L)
+    q = seeded_normal(gen, (14, 24, 128))
+    seq = torch.tensor([9000, 3000])
+    plain = decode(gpu_ops, cache, q, table, seq, 7)
+    bt, sl, qd = table.to(DEV), seq.to(device=DEV, dtype=torch.int32), q.to(DEV)
+    nbytes = gpu_ops.attn_workspace_bytes(2, bt.shape[1], 1, 7, 4, 128)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=DEV)
+    out = torch.full(q.shape, float("nan"), dtype=torch.float16, device=DEV)
+    call = gpu_ops.bind_int8k_int4v_attn_batch(qd, None, None, *cache.region_args(), bt, sl, None, ws,
+                                               None, None, None, out, 7, 1)
+    call()
+    torch.cuda.synchronize()
+    assert max_abs(out, plain) == 0.0
+    out.fill_(float("nan"))
+    call(stages=1)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all(), "split-only stage wrote the output"
+    call(stages=2)
+    torch.cuda.synchronize()
+    assert max_abs(out, plain) == 0.0
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()  # creates the event handle
+    out.fill_(float("nan"))
+    call(split_done_event=ev.cuda_event)
+    torch.cuda.synchronize()
+    assert max_abs(out, plain) == 0.0
+    # New lengths in the same storage are read at launch time.
+    sl.copy_(torch.tensor([2500, 1000], dtype=torch.int32))
+    call()
+    torch.cuda.synchronize()
+    again = decode(gpu_ops, cache, q, table, torch.tensor([2500, 1000]), 7)
+    assert max_abs(out, again) == 0.0
+    with pytest.raises(RuntimeError, match="stages"):
+        call(stages=0)

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from k8v4_v030.cache_views import bind_regions
-from k8v4_v030.layout import PageLayout
+from k8v4_v030.layout import PAGE, PageLayout
 from oracle import paged
 
 pytestmark = pytest.mark.gpu
@@ -166,3 +166,21 @@ def test_store_config2_full_size(gpu_ops):
     # Every other page is untouched.
     untouched_count = int((raw.view(pool, page_bytes) != MARK).any(dim=1).sum())
     assert untouched_count == len(touched)
+
+
+def test_bound_store_matches_the_plain_op(gpu_ops):
+    lay = PageLayout(4, 128)
+    geom = paged.Geometry(4, 128)
+    k, v = _seeded_kv(77, 300, 4, 128)
+    slots = torch.randperm(20 * PAGE, generator=torch.Generator().manual_seed(78))[:300]
+    a, va = _cache(20, lay)
+    b, vb = _cache(20, lay)
+    _store(gpu_ops, va, k.to(DEV), v.to(DEV), slots.to(DEV))
+    call = gpu_ops.bind_kv_store_paged(k.to(DEV), v.to(DEV), slots.to(DEV), vb["k"], vb["k_scale"], vb["v"],
+                                       vb["v_scale"], vb["v_zero"])
+    call()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert np.array_equal(b.view(torch.uint8).cpu().numpy(), _oracle_blob(20, geom, k, v, slots))
+    assert gpu_ops.bind_kv_store_paged(k[:0].to(DEV), v[:0].to(DEV), slots[:0].to(DEV), vb["k"], vb["k_scale"],
+                                       vb["v"], vb["v_scale"], vb["v_zero"]) is None
