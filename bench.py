@@ -38,6 +38,7 @@ for _p in (str(REPO / "k8v4-xpu_amd"), str(REPO)):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 METRIC = "K8V4 paged-decode HBM GB/s (% of peak) + µs/layer at 4 seqs×128K ctx"
 TRAFFIC_PROFILE = REPO / "profiles" / "decode_split_kernel_headline_traffic.md"
 PAGE = 64
@@ -203,6 +204,39 @@ class StoreWorkload:
         self.inputs[i % len(self.inputs)]()
 
 
+class PrefillWorkload:
+    """A 4,224-token query chunk over 131,072 cached tokens plus itself (one sequence)."""
+
+    def __init__(self, ops, torch, *, cached=131072, chunk=4224, hkv=4, head_dim=128, seed=1005):
+        import math
+
+        from k8v4_v030.cache_views import bind_regions
+        from k8v4_v030.layout import PageLayout
+
+        self.layout = PageLayout(hkv, head_dim)
+        self.seq_len, self.q_len = cached + chunk, chunk
+        pages = -(-self.seq_len // PAGE)
+        self.num_pages = pages
+        self.raw = torch.empty(pages * self.layout.page_bytes, dtype=torch.int8, device="cuda")
+        self.views = bind_regions(self.raw, self.layout)
+        # The chunk's own K/V go through the store kernel like the cached prefix.
+        fill_pool(ops, torch, self.views, pages, hkv, head_dim, seed)
+        gen = torch.Generator().manual_seed(seed)
+        self.row = torch.randperm(pages, generator=gen).to(torch.int32).to("cuda")
+        qgen = torch.Generator(device="cuda").manual_seed(seed + 1)
+        self.q = torch.randn((chunk, 6 * hkv, head_dim), generator=qgen, dtype=torch.float16, device="cuda")
+        self.out = torch.empty_like(self.q)
+        v = self.views
+        self.call = ops.bind_prefill_paged(self.q, v["k"], v["k_scale"], v["v"], v["v_scale"], v["v_zero"],
+                                           self.row, self.seq_len, 1, 1.0 / math.sqrt(head_dim), self.out)
+        # Unmasked (query, key) pairs: query j sees cached + j + 1 keys.
+        pairs = chunk * (cached + 1) + chunk * (chunk - 1) // 2
+        self.flops = pairs * 6 * hkv * 4 * head_dim
+
+    def launch(self, i: int, split_done=None, stages=3):
+        self.call()
+
+
 # --------------------------------------------------------------------- timing
 def progress(msg: str) -> None:
     print("[bench] " + msg, file=sys.stderr, flush=True)
@@ -350,7 +384,20 @@ def config_rows(torch, hip, ops, steps, warmup):
     decode_row("3_mtp_verify_4x8192_q7", [8192] * 4, 7, copies=12, seed=1003, pool_pages_per_copy=1024)
     decode_row("4_mixed_long_q7", [2048, 32768, 131072, 200000], 7, copies=3, seed=1004,
                shared_prefix_pages=1024)
-    rows["5_prefill_4224_over_131072"] = {"status": "not built"}
+    w = PrefillWorkload(ops, torch)
+    us = kernel_us(torch, hip, w, 3, max(5, steps // 10), 2)
+    tflops = w.flops / (us * 1e-6) / 1e12
+    rows["5_prefill_4224_over_131072"] = {
+        "us_per_layer": round(us, 1),
+        "algorithmic_flops": w.flops,
+        "TFLOPs": round(tflops, 1),
+        "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
+        "mfma_utilization": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "dtype": "f16 MFMA (exact K codes / V nibbles), f32 accumulation",
+    }
+    del w
+    torch.cuda.empty_cache()
+    progress("5_prefill_4224_over_131072: %.1f us/layer, %.1f TFLOP/s" % (us, tflops))
     decode_row("reference_shape_d256_hkv2_ctx127853_q7", [127853], 7, copies=4, seed=1007,
                hkv=2, head_dim=256)
     return rows

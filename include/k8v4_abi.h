@@ -117,6 +117,33 @@ int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
                              int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
                              int num_splits, void *stream, void *split_done_event, int stages);
 
+/*
+ * Chunked prefill of one sequence over the quantized cache (replaces the
+ * prefill paths of k8v4_v030: eager_prefill, dequant.py:213-242;
+ * head_major_prefill, onednn_prefill.py:188-241; and the fused fp16 SDPA it
+ * calls, torch.ops.k8v4_sdpa.sdpa_len, native/k8v4_sdpa.cpp:232-238).
+ *
+ * q:   [q_len, 6*hkv, head_dim] (K8V4_F16 or K8V4_BF16, bf16 is rounded to
+ *      fp16 first), token stride q_tok_stride elements (multiple of 8, base
+ *      16-byte aligned); not quantized.
+ * block_row: int32 [table_width] table row of the sequence (entry e covers
+ *      kernel pages e*pages_per_block .. +pages_per_block-1).
+ * Query row j is token seq_len - q_len + j and attends to keys
+ * t <= seq_len - q_len + j (bottom-right causal); K and V are the cache's
+ * codes dequantized exactly as dequant.py:96-106; softmax(scale * q.k),
+ * fp32 accumulation.
+ * out: [q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride
+ *      (multiple of 4, base 16-byte aligned).
+ * q_len == 0 is a no-op; q_len > seq_len is an error.
+ */
+int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                       const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                       const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                       int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                       int64_t vz_page_stride, const int32_t *block_row, int64_t table_width,
+                       int pages_per_block, int64_t seq_len, int64_t q_len, int hkv, int head_dim,
+                       float scale, void *out, int out_dtype, int64_t out_tok_stride, void *stream);
+
 /* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
  * No counterpart in the reference (its caller sized [nprog, 64, D] fp32
  * partials, k8v4_v030/scratch.py:34-45, which is always at least this). */

@@ -1,0 +1,533 @@
+// Chunked-prefill attention over the int8-K / int4-V paged cache.
+//
+// Reference semantics: the eager prefill k8v4_v030/dequant.py:213-242
+// (gather + dequantize K = code * k_scale, V = (nibble - v_zero) * v_scale,
+// then softmax(Q K^T * scale) V) with the bottom-right causal rule of
+// dequant.py:245-261 / onednn_prefill.py:89-121: query row j of a q_len
+// suffix is token seq_len - q_len + j and sees keys t <= that position.  Q is
+// not quantized; accumulation is fp32.
+//
+// MI355X design:
+//  * The problem of one KV head is a matrix of q_len * 6 query rows (token
+//    major, the 6 GQA heads of a token adjacent) against seq_len keys.  A
+//    work-group owns a block of rows of one KV head and streams every page of
+//    that head once: direct-to-LDS loads stage the next page's codes while the
+//    current page is computed, then the group converts them into the other
+//    buffer of a two-buffer MFMA tile ring.  Each page is a 64-key tile shared
+//    by all waves (all GQA rows) of the group.
+//  * Dequantization is split so the per-element work is shared by the whole
+//    work-group and exact: K codes become fp16 integers (byte permute into the
+//    mantissa of 1024.0, then subtract 1152), the K scale is applied to the
+//    score column; V nibbles become fp16 subnormals (n * 2^-24 for even dims,
+//    16 n * 2^-24 for odd dims) in a transposed tile, the V scale multiplies
+//    P and the zero point is subtracted once per row at the end:
+//      sum_t p_t (n_t - z_t) s_t = sum_t (p_t s_t) n_t - sum_t (p_t s_t) z_t.
+//  * S^T = K Q^T and O^T = V^T P'^T on v_mfma_f32_16x16x32_f16: the query row
+//    is the MFMA column, so each lane owns one row's softmax state and the
+//    score tile is already the B operand of the PV product.
+//  * Online softmax in the exp2 domain with a lazy rescale (the running max
+//    only moves when a row's max grows by more than 2^8).
+#include "k8v4_common.h"
+
+namespace k8v4 {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+constexpr float kThreshold = 8.0f;
+constexpr int kThreads = 256;  // four waves
+constexpr uint32_t kEvenNib = 0x000F000Fu;
+constexpr uint32_t kOddNib = 0x00F000F0u;
+
+struct PrefillArgs {
+  const uint16_t *q;
+  int64_t q_tok_stride;  // elements; head stride is head_dim
+  int q_bf16;
+  const int8_t *k_cache;
+  const float *k_scale;
+  const uint8_t *v_cache;
+  const float *v_scale;
+  const float *v_zero;
+  int64_t num_pages;
+  int64_t k_ps, ks_ps, v_ps, vs_ps, vz_ps;  // page strides, bytes
+  const int32_t *block_row;
+  int ppb;
+  int seq_len;
+  int q_len;
+  int hkv;
+  float c;       // softmax scale * log2(e)
+  int blocks;    // row blocks per KV head
+  int per_xcd;   // row blocks interleaved per XCD group (0: plain order)
+  void *out;
+  int out_dtype;
+  int64_t out_tok_stride;  // elements
+};
+
+template <int D>
+struct Tile {
+  static constexpr int RT = D == 128 ? 2 : 1;        // 16-row MFMA tiles per wave
+  static constexpr int WPE = D == 128 ? 2 : 1;       // waves per SIMD (LDS: one group per CU at D=256)
+  static constexpr int ROWS = 4 * 16 * RT;           // query rows per work-group
+  static constexpr int DS = D / 32;                  // k-steps of the QK MFMA
+  static constexpr int DT = D / 16;                  // 16-dim output tiles
+  // MFMA tile of one page (one ring buffer).  Row paddings, not XOR
+  // swizzles, keep the operand reads conflict-free, so every read address is
+  // one per-lane base plus a compile-time offset.
+  static constexpr int KROW = 2 * D + 16;            // K row: D fp16 codes + 16 B (8 rows hit 8 bank groups)
+  static constexpr int K_BYTES = 64 * KROW;
+  static constexpr int V_OFF = K_BYTES;              // V^T: row d = 64 keys fp16 (8-byte chunks XOR d%16)
+  static constexpr int VBLK = 16 * 128 + 8;          // 16 rows, then 8 B of padding
+  static constexpr int S_OFF = V_OFF + (D / 16) * VBLK;  // ksc[64] | vs[64] | vz[64] floats
+  static constexpr int BUF = S_OFF + 768;
+  // Staging of the next page's raw codes: [64][D] K | [64][D/2] V (its scale
+  // planes go straight into the S area of the ring buffer they belong to).
+  static constexpr int SV_OFF = 64 * D;
+  static constexpr int STAGE = SV_OFF + 32 * D;
+  static constexpr int KCH = 64 * D / 16 / kThreads;   // 16-byte K pieces per thread
+  static constexpr int VCH = 32 * D / 16 / kThreads;   // 16-byte V pieces per thread
+  static constexpr int VIT = 32 * (D / 16) / kThreads;  // (key pair, 8-byte group) items per thread
+};
+
+template <int D>
+__device__ __forceinline__ int vt_offset(int d, int chunk) {
+  return (d >> 4) * Tile<D>::VBLK + (d & 15) * 128 + ((chunk ^ (d & 15)) * 8);
+}
+
+typedef const __attribute__((address_space(4))) int32_t *const_i32_ptr;
+
+__device__ __forceinline__ int64_t page_of(const PrefillArgs &a, int p) {
+  const const_i32_ptr row = (const_i32_ptr)(a.block_row);
+  int64_t phys = a.ppb <= 1 ? row[p] : static_cast<int64_t>(row[p / a.ppb]) * a.ppb + (p % a.ppb);
+  if (phys < 0 || phys >= a.num_pages) phys = 0;  // stay in bounds on a bad table entry
+  return phys;
+}
+
+// ---- page staging: direct-to-LDS loads of one page of one head (no registers
+// held while the previous page is computed), then a work-group pass that
+// converts the staged codes into the MFMA tile of the next ring buffer.
+typedef __attribute__((address_space(3))) char lds_t;
+
+__device__ __forceinline__ void dma16(const void *src, lds_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *src, lds_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 4, 0, 0);
+}
+
+// Wave w, lane L: 16-byte K pieces 64 * (4 j + w) + L (row-major codes), V
+// pieces likewise, and scale plane w (waves 0-2) for key L, the latter into the
+// S area of the ring buffer the page will be converted into.
+template <int D>
+__device__ __forceinline__ void stage_page(const PrefillArgs &a, int p, int h, int wave, int lane, lds_t *stage,
+                                           lds_t *scales) {
+  using T = Tile<D>;
+  const int64_t phys = page_of(a, p);
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + h * D;
+  const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps + h * (D / 2);
+#pragma unroll
+  for (int j = 0; j < T::KCH; ++j) {
+    const int c = 64 * (4 * j + wave) + lane;
+    const int key = c / (D / 16), part = c % (D / 16);
+    dma16(kb + static_cast<int64_t>(key) * a.hkv * D + part * 16, stage + 1024 * (4 * j + wave));
+  }
+#pragma unroll
+  for (int j = 0; j < T::VCH; ++j) {
+    const int c = 64 * (4 * j + wave) + lane;
+    const int key = c / (D / 32), part = c % (D / 32);
+    dma16(vb + static_cast<int64_t>(key) * a.hkv * (D / 2) + part * 16, stage + T::SV_OFF + 1024 * (4 * j + wave));
+  }
+  if (wave < 3) {
+    const float *plane = wave == 0 ? a.k_scale : wave == 1 ? a.v_scale : a.v_zero;
+    const int64_t ps = wave == 0 ? a.ks_ps : wave == 1 ? a.vs_ps : a.vz_ps;
+    const char *src = reinterpret_cast<const char *>(plane) + phys * ps + (static_cast<int64_t>(lane) * a.hkv + h) * 4;
+    dma4(src, scales + 256 * wave);
+  }
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// int8 codes (4 per dword) -> exact fp16 integers.
+__device__ __forceinline__ void k_codes_to_f16(uint32_t w, v2h &lo, v2h &hi) {
+  const uint32_t u = w ^ 0x80808080u;  // biased: code + 128
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const v2h bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = __builtin_bit_cast(v2h, a) - bias;
+  hi = __builtin_bit_cast(v2h, b) - bias;
+}
+
+template <int D>
+__device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const char *stage, char *buf, int tid) {
+  using T = Tile<D>;
+#pragma unroll
+  for (int j = 0; j < T::KCH; ++j) {
+    const int c = tid + kThreads * j;
+    const int key = c / (D / 16), part = c % (D / 16);
+    const uint4 w = *reinterpret_cast<const uint4 *>(stage + 16 * c);
+    v2h h[8];
+    k_codes_to_f16(w.x, h[0], h[1]);
+    k_codes_to_f16(w.y, h[2], h[3]);
+    k_codes_to_f16(w.z, h[4], h[5]);
+    k_codes_to_f16(w.w, h[6], h[7]);
+    char *row = buf + key * T::KROW;
+    const uint4 c0 = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
+                                __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
+    const uint4 c1 = make_uint4(__builtin_bit_cast(uint32_t, h[4]), __builtin_bit_cast(uint32_t, h[5]),
+                                __builtin_bit_cast(uint32_t, h[6]), __builtin_bit_cast(uint32_t, h[7]));
+    *reinterpret_cast<uint4 *>(row + 32 * part) = c0;
+    *reinterpret_cast<uint4 *>(row + 32 * part + 16) = c1;
+  }
+#pragma unroll
+  for (int j = 0; j < T::VIT; ++j) {
+    const int it = tid + kThreads * j;
+    const int pair = it / (D / 16), grp = it % (D / 16);
+    const uint2 v0 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair) * (D / 2) + 8 * grp);
+    const uint2 v1 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair + 1) * (D / 2) + 8 * grp);
+    const int chunk = pair >> 1, word = (pair & 1) * 4;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint32_t w0 = b < 4 ? v0.x : v0.y;
+      const uint32_t w1 = b < 4 ? v1.x : v1.y;
+      const uint32_t sel = 0x0C000C00u | ((4u + (b & 3)) << 16) | (b & 3);
+      const uint32_t x = __builtin_amdgcn_perm(w1, w0, sel);  // byte b of both keys, one per 16-bit half
+      const int d = 16 * grp + 2 * b;
+      char *ve = buf + T::V_OFF + vt_offset<D>(d, chunk) + word;
+      char *vo = buf + T::V_OFF + vt_offset<D>(d + 1, chunk) + word;
+      *reinterpret_cast<uint32_t *>(ve) = x & kEvenNib;
+      *reinterpret_cast<uint32_t *>(vo) = x & kOddNib;
+    }
+  }
+  if (tid < 64) {
+    float *s = reinterpret_cast<float *>(buf + T::S_OFF);
+    // Keys past the sequence may hold anything (unwritten planes): zero them
+    // so a masked probability never meets a NaN scale.
+    const bool live = p * 64 + tid < a.seq_len;
+    s[tid] = live ? s[tid] * a.c : 0.f;
+    s[64 + tid] = live ? s[64 + tid] : 0.f;
+    s[128 + tid] = live ? s[128 + tid] : 0.f;
+  }
+}
+
+__device__ __forceinline__ float xlane_max16_32(float x) {
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ float xlane_sum16_32(float x) {
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+__device__ __forceinline__ void store_out4(void *out, int dtype, int64_t idx, v4f v) {
+  if (dtype == K8V4_F32) {
+    *reinterpret_cast<v4f *>(static_cast<float *>(out) + idx) = v;
+  } else if (dtype == K8V4_BF16) {
+    __bf16 *o = static_cast<__bf16 *>(out) + idx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = static_cast<__bf16>(v[i]);
+  } else {
+    const v4h h = __builtin_convertvector(v, v4h);
+    *reinterpret_cast<v4h *>(static_cast<_Float16 *>(out) + idx) = h;
+  }
+}
+
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
+prefill_kernel(PrefillArgs a) {
+  using T = Tile<D>;
+  constexpr int RT = T::RT;
+  __shared__ __attribute__((aligned(16))) char smem[2 * T::BUF + T::STAGE];
+  lds_t *stage_lds = (lds_t *)(smem + 2 * T::BUF);
+  const char *stage = smem + 2 * T::BUF;
+
+  // Work-group -> (KV head, row block).  With per_xcd > 0 the ids that land
+  // on one XCD (id % 8) all belong to one KV head, so its L2 holds one stream.
+  int h, rb;
+  const int id = blockIdx.x;
+  if (a.per_xcd > 0) {
+    h = (id % 8) / a.per_xcd;
+    rb = (id / 8) * a.per_xcd + (id % 8) % a.per_xcd;
+  } else {
+    h = id / a.blocks;
+    rb = id % a.blocks;
+  }
+  if (h >= a.hkv || rb >= a.blocks) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64, g = lane / 16, r16 = lane % 16;
+  const int nrows = a.q_len * 6;
+  const int row0 = rb * T::ROWS;
+
+  // ---- query fragments (B operand of S^T = K Q^T) and row limits
+  v8h qf[RT][T::DS];
+  int lim[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = row0 + wave * 16 * RT + rt * 16 + r16;
+    const bool valid = row < nrows;
+    const int tok = valid ? row / 6 : 0;
+    const int qh = h * 6 + (valid ? row % 6 : 0);
+    // A padding row sees key 0 only, which keeps its softmax finite.
+    lim[rt] = valid ? a.seq_len - a.q_len + tok + 1 : 1;
+    const uint16_t *src = a.q + static_cast<int64_t>(tok) * a.q_tok_stride + static_cast<int64_t>(qh) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < T::DS; ++ds) {
+      const uint4 raw = valid ? *reinterpret_cast<const uint4 *>(src + 32 * ds) : make_uint4(0, 0, 0, 0);
+      if (a.q_bf16) {
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qf[rt][ds][2 * e] = static_cast<_Float16>(__uint_as_float(w[e] << 16));
+          qf[rt][ds][2 * e + 1] = static_cast<_Float16>(__uint_as_float(w[e] & 0xFFFF0000u));
+        }
+      } else {
+        qf[rt][ds] = __builtin_bit_cast(v8h, raw);
+      }
+    }
+  }
+
+  // Keys this work-group needs, and the pages that need no causal mask.
+  const int tok_lo = row0 / 6;
+  const int tok_hi = min(a.q_len - 1, (row0 + T::ROWS - 1) / 6);
+  const int key_end = a.seq_len - a.q_len + tok_hi + 1;
+  const int npages = (key_end + 63) / 64;
+  const int full_pages = (a.seq_len - a.q_len + tok_lo + 1) / 64;
+
+  v4f O[T::DT][RT];
+  float m_run[RT], lsum[RT], corr[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] = -INFINITY;
+    lsum[rt] = 0.f;
+    corr[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < T::DT; ++dt) O[dt][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+
+  stage_page<D>(a, 0, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
+  wait_dma();
+  __syncthreads();
+  convert_page<D>(a, 0, stage, smem, tid);
+  __syncthreads();
+
+  for (int p = 0; p < npages; ++p) {
+    const char *buf = smem + (p & 1) * T::BUF;
+    const bool more = p + 1 < npages;
+    if (more) stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + ((p + 1) & 1) * T::BUF + T::S_OFF));
+
+    // ---- S^T = K Q^T for the 64 keys of page p
+    v4f S[4][RT];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const char *krow = buf + (16 * kt + r16) * T::KROW;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) S[kt][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < T::DS; ++ds) {
+        const v8h kf = *reinterpret_cast<const v8h *>(krow + (4 * ds + g) * 16);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          S[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[rt][ds], S[kt][rt], 0, 0, 0);
+      }
+    }
+
+    // ---- scaled scores, masks, lazy max
+    const float *sc = reinterpret_cast<const float *>(buf + T::S_OFF);
+    const bool masked = p >= full_pages;
+    float mx[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) mx[rt] = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const v4f ksc = *reinterpret_cast<const v4f *>(sc + 16 * kt + 4 * g);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = S[kt][rt][i] * ksc[i];
+          if (masked) {
+            const int key = p * 64 + 16 * kt + 4 * g + i;
+            x = key < lim[rt] ? x : -INFINITY;
+          }
+          S[kt][rt][i] = x;
+          mx[rt] = fmaxf(mx[rt], x);
+        }
+    }
+    bool grow = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      mx[rt] = xlane_max16_32(mx[rt]);
+      grow |= mx[rt] > m_run[rt] + kThreshold;
+    }
+    if (__ballot(grow)) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const float mnew = fmaxf(m_run[rt], mx[rt]);
+        const float alpha = m_run[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rt] - mnew);
+        m_run[rt] = mnew;
+        lsum[rt] *= alpha;
+        corr[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < T::DT; ++dt) O[dt][rt] *= alpha;
+      }
+    }
+
+    // ---- P' = exp2(x - m) * v_scale as the fp16 B operand; row sums and zero-point terms
+    v8h pb[2][RT];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const v4f vsc = *reinterpret_cast<const v4f *>(sc + 64 + 16 * kt + 4 * g);
+      const v4f vzc = *reinterpret_cast<const v4f *>(sc + 128 + 16 * kt + 4 * g);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(S[kt][rt][i] - m_run[rt]);
+          lsum[rt] += pr;
+          const float pv = pr * vsc[i];
+          corr[rt] = fmaf(pv, vzc[i], corr[rt]);
+          pb[kt >> 1][rt][4 * (kt & 1) + i] = static_cast<_Float16>(pv);
+        }
+    }
+
+    // ---- O^T += V^T P'^T
+    const char *vbase = buf + T::V_OFF;
+#pragma unroll
+    for (int dt = 0; dt < T::DT; ++dt) {
+      const int d = 16 * dt + r16;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + vt_offset<D>(d, 8 * s + g));
+        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + vt_offset<D>(d, 8 * s + 4 + g));
+        const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const v8h vf = __builtin_bit_cast(v8h, w);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          O[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[s][rt], O[dt][rt], 0, 0, 0);
+      }
+    }
+
+    if (more) {
+      wait_dma();
+      __syncthreads();
+      convert_page<D>(a, p + 1, stage, smem + ((p + 1) & 1) * T::BUF, tid);
+    }
+    __syncthreads();
+  }
+
+  // ---- finalize: O = (acc * 2^24|2^20 - corr) / l, written as [token][head][D]
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = row0 + wave * 16 * RT + rt * 16 + r16;
+    const float l = xlane_sum16_32(lsum[rt]);
+    const float cz = xlane_sum16_32(corr[rt]);
+    if (row >= nrows) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int tok = row / 6, qh = h * 6 + row % 6;
+    const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < T::DT; ++dt) {
+      v4f o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (O[dt][rt][i] * ((i & 1) ? 1048576.f : 16777216.f) - cz) * inv;
+      store_out4(a.out, a.out_dtype, ob + 16 * dt, o);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                                  const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                                  const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                                  int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                                  int64_t vz_page_stride, const int32_t *block_row, int64_t table_width,
+                                  int pages_per_block, int64_t seq_len, int64_t q_len, int hkv, int head_dim,
+                                  float scale, void *out, int out_dtype, int64_t out_tok_stride, void *stream) {
+  using namespace k8v4;
+  clear_error();
+  K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
+  K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)", head_dim);
+  K8V4_REQUIRE(q_len >= 0 && seq_len >= 0 && seq_len < (int64_t(1) << 30), "bad lengths");
+  K8V4_REQUIRE(q_len <= seq_len, "query longer than the KV sequence");
+  if (q_len == 0) return K8V4_OK;
+  K8V4_REQUIRE(pages_per_block >= 1, "pages_per_block");
+  K8V4_REQUIRE(num_pages >= 1, "empty cache");
+  K8V4_REQUIRE(table_width >= 1 && table_width * pages_per_block * kPage >= seq_len,
+               "block table row covers %lld tokens, seq_len is %lld",
+               static_cast<long long>(table_width * pages_per_block * kPage), static_cast<long long>(seq_len));
+  K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
+  K8V4_REQUIRE(out_dtype == K8V4_F16 || out_dtype == K8V4_BF16 || out_dtype == K8V4_F32,
+               "out dtype must be fp16, bf16 or fp32");
+  K8V4_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && v_zero && block_row && out, "null pointer");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
+               "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
+  K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+  K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim && out_tok_stride % 4 == 0,
+               "out token stride must cover HQ*D and be a multiple of 4");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, "out must be 16-byte aligned");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && k_page_stride % 16 == 0,
+               "k_cache must keep 16-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(v_cache) % 8 == 0 && v_page_stride % 8 == 0,
+               "v_cache must keep 8-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_scale) % 4 == 0 && reinterpret_cast<uintptr_t>(v_scale) % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(v_zero) % 4 == 0 && ks_page_stride % 4 == 0 &&
+                   vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
+               "scale planes must be 4-byte aligned");
+  K8V4_REQUIRE(scale > 0.f && scale < 1e30f, "softmax scale must be positive and finite");
+
+  PrefillArgs a;
+  a.q = static_cast<const uint16_t *>(q);
+  a.q_tok_stride = q_tok_stride;
+  a.q_bf16 = q_dtype == K8V4_BF16;
+  a.k_cache = k_cache;
+  a.k_scale = k_scale;
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.v_zero = v_zero;
+  a.num_pages = num_pages;
+  a.k_ps = k_page_stride;
+  a.ks_ps = ks_page_stride;
+  a.v_ps = v_page_stride;
+  a.vs_ps = vs_page_stride;
+  a.vz_ps = vz_page_stride;
+  a.block_row = block_row;
+  a.ppb = pages_per_block;
+  a.seq_len = static_cast<int>(seq_len);
+  a.q_len = static_cast<int>(q_len);
+  a.hkv = hkv;
+  a.c = scale * 1.4426950408889634f;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.out_tok_stride = out_tok_stride;
+
+  const int rows_per_group = head_dim == 128 ? Tile<128>::ROWS : Tile<256>::ROWS;
+  const int64_t blocks = (q_len * kGqa + rows_per_group - 1) / rows_per_group;
+  K8V4_REQUIRE(blocks * hkv < (int64_t(1) << 31), "query chunk too long");
+  a.blocks = static_cast<int>(blocks);
+  int64_t grid;
+  const int per = 8 / hkv;  // row blocks of one head that share an XCD id group
+  if (blocks >= per) {
+    a.per_xcd = per;
+    const int64_t padded = (blocks + per - 1) / per * per;
+    grid = padded * hkv;
+  } else {
+    a.per_xcd = 0;
+    grid = blocks * hkv;
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    prefill_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(a);
+  else
+    prefill_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(a);
+  return launch_status("k8v4_prefill_paged");
+}

@@ -67,6 +67,12 @@ _EXTRA_SYMBOLS: list[tuple[str, list, object]] = [
     ("k8v4_attn_workspace_bytes", [_i64, _i64, _i32, _i32, _i32, _i32, _i32], _i64),
 ]
 _EXTRA_SYMBOLS.append(("k8v4_attn_batch_profiled", _EXTRA_SYMBOLS[0][1] + [_vp, _i32], _i32))
+_EXTRA_SYMBOLS.append((
+    "k8v4_prefill_paged",
+    [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+     _vp, _i64, _i32, _i64, _i64, _i32, _i32, ctypes.c_float, _vp, _i32, _i64, _vp],
+    _i32,
+))
 
 
 def load_library():
@@ -325,6 +331,51 @@ class _Ops:
         keep = tensors + ((visible_lens,) if vis_ptr else ())
         return BoundCall(self._lib, self._lib.k8v4_attn_batch, args, dev, keep,
                          profiled=self._lib.k8v4_attn_batch_profiled)
+
+    # -- chunked prefill ----------------------------------------------------
+    def prefill_paged(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len: int,
+                      pages_per_block: int, scale: float, out):
+        """Bottom-right causal attention of ``q [q_len, HQ, D]`` over one sequence's pages into ``out``."""
+        call = self.bind_prefill_paged(q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len,
+                                       pages_per_block, scale, out)
+        if call is not None:
+            call()
+
+    def bind_prefill_paged(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len: int,
+                           pages_per_block: int, scale: float, out):
+        """Validate one prefill; returns a :class:`BoundCall` (None when ``q_len`` is 0)."""
+        _require(q.dim() == 3, "query [T,HQ,D]")
+        head_dim = int(q.shape[2])
+        _require(head_dim in (128, 256), "query [T,HQ,D] with D in (128, 256)")
+        hkv = int(k_cache.shape[2]) if k_cache.dim() == 4 else -1
+        _require(int(q.shape[1]) == GQA * hkv,
+                 "query has %d heads, the K8/V4 cache holds %d (needs %d)" % (int(q.shape[1]), hkv, GQA * hkv))
+        _checked_hkv(hkv)
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        q_len, seq_len = int(q.shape[0]), int(seq_len)
+        if q_len > seq_len:
+            raise RuntimeError("query longer than the KV sequence")
+        if q_len == 0:
+            return None
+        _require(q.dtype in (torch.float16, torch.bfloat16), "query must be float16 or bfloat16")
+        _require(q.stride(2) == 1 and q.stride(1) == head_dim, "query head/dim strides")
+        _require(out.shape == q.shape, "out shape")
+        _require(out.dtype in (torch.float16, torch.bfloat16, torch.float32), "out float16, bfloat16 or float32")
+        _require(out.stride(2) == 1 and out.stride(1) == head_dim, "out head/dim strides")
+        _require(block_row.dtype == torch.int32 and block_row.dim() == 1 and block_row.stride(0) == 1,
+                 "block_row must be a contiguous int32 [width] row")
+        _require(int(pages_per_block) >= 1, "pages_per_block")
+        tensors = (q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, out)
+        dev = _on_gpu(*tensors)
+        args = [
+            _ptr(q), _DTYPE_CODE[q.dtype], int(q.stride(0)) if q_len > 1 else GQA * hkv * head_dim,
+            *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
+            _ptr(block_row), int(block_row.shape[0]), int(pages_per_block), seq_len, q_len, hkv, head_dim,
+            float(scale), _ptr(out), _DTYPE_CODE[out.dtype],
+            int(out.stride(0)) if q_len > 1 else GQA * hkv * head_dim,
+        ]
+        return BoundCall(self._lib, self._lib.k8v4_prefill_paged, args, dev, tensors)
 
     def k_store_paged(self, *args, **kwargs):
         raise RuntimeError("k_store_paged: use kv_store_paged (K and V are written by one kernel)")

@@ -1,0 +1,143 @@
+"""Chunked-prefill kernel vs the oracle (GPU).
+
+The oracle (oracle/attention.py prefill_attention) is textbook bottom-right
+causal softmax attention in float64 over the fp32-dequantized cache, itself
+pinned to torch's scaled_dot_product_attention (tests/test_oracle.py).
+Tolerance: max-abs 2e-3 with a 1e-2 relative allowance.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_cases import DEV, Cache, assert_close, fill_sequence, random_tables, seeded_normal
+from k8v4_v030.layout import PAGE, PageLayout
+from k8v4_v030.prefill import hip_prefill
+from oracle import attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(cache, q, row, seq_len, ppb=1, out_dtype=None, scale=None):
+    scale = 1.0 / math.sqrt(cache.layout.head_dim) if scale is None else scale
+    qd = q.to(DEV)
+    out = torch.full(q.shape, float("nan"), dtype=out_dtype or q.dtype, device=DEV)
+    got = hip_prefill(qd, cache.views, row.to(device=DEV, dtype=torch.int32), seq_len, ppb, scale, out=out)
+    torch.cuda.synchronize()
+    return got
+
+
+def _oracle(cache, q, row, seq_len, ppb=1, rows=None, scale=None):
+    scale = 1.0 / math.sqrt(cache.layout.head_dim) if scale is None else scale
+    return attention.prefill_attention(q.float().cpu().numpy(), cache.blob(), cache.geom, row.numpy(), seq_len,
+                                       ppb, scale, rows=rows)
+
+
+@pytest.mark.parametrize("hkv,d,q_len,seq_len", [
+    (4, 128, 1, 1), (4, 128, 7, 300), (4, 128, 64, 64), (4, 128, 100, 1000), (2, 128, 33, 2049),
+    (4, 128, 250, 4000), (2, 256, 20, 500), (4, 256, 70, 700), (2, 256, 1, 129),
+])
+def test_prefill_matches_oracle(gpu_ops, hkv, d, q_len, seq_len):
+    print("prefill hkv=%d d=%d q=%d seq=%d" % (hkv, d, q_len, seq_len), flush=True)
+    lay = PageLayout(hkv, d)
+    gen = torch.Generator().manual_seed(7 * q_len + seq_len + d + hkv)
+    pool = (seq_len + PAGE - 1) // PAGE + 5
+    table = random_tables(gen, [seq_len], pool)
+    cache = Cache(pool, lay)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len)
+    q = seeded_normal(gen, (q_len, lay.hq, d))
+    got = _run(cache, q, table[0], seq_len).float().cpu().numpy()
+    err = assert_close(got, _oracle(cache, q, table[0], seq_len), what="prefill")
+    print("  max abs err %.2e" % err, flush=True)
+
+
+def test_prefill_manager_blocks_and_dirty_tail(gpu_ops):
+    """ppb=2 tables; the tail of the last page holds garbage codes and NaN planes."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(5)
+    seq_len, q_len, ppb = 1000, 90, 2
+    cache = Cache(64, lay)
+    table = random_tables(gen, [seq_len], 64, ppb=ppb)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len, ppb=ppb)
+    last = (seq_len - 1) // PAGE
+    phys = int(table[0][last // ppb]) * ppb + last % ppb
+    tail = slice(seq_len % PAGE, PAGE)
+    cache.views["k"][phys, tail] = 77
+    cache.views["v"][phys, tail] = 0xEE
+    for plane in ("k_scale", "v_scale", "v_zero"):
+        cache.views[plane][phys, tail] = float("nan")
+    q = seeded_normal(gen, (q_len, 24, 128))
+    got = _run(cache, q, table[0], seq_len, ppb=ppb).float().cpu().numpy()
+    assert_close(got, _oracle(cache, q, table[0], seq_len, ppb=ppb), what="dirty tail")
+
+
+def test_prefill_dtypes(gpu_ops):
+    lay = PageLayout(2, 128)
+    gen = torch.Generator().manual_seed(11)
+    seq_len, q_len = 700, 50
+    cache = Cache(20, lay)
+    table = random_tables(gen, [seq_len], 20)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len)
+    q = seeded_normal(gen, (q_len, 12, 128))
+    want = _oracle(cache, q, table[0], seq_len)
+    for out_dtype, tol in ((torch.float32, 2e-3), (torch.bfloat16, 8e-3)):
+        got = _run(cache, q, table[0], seq_len, out_dtype=out_dtype)
+        assert got.dtype == out_dtype
+        assert_close(got.float().cpu().numpy(), want, atol=tol, what=str(out_dtype))
+    # bf16 queries are rounded to fp16 like the reference's query.to(float16).
+    qb = q.to(torch.bfloat16)
+    got = _run(cache, qb, table[0], seq_len)
+    assert got.dtype == torch.bfloat16
+    want_b = _oracle(cache, qb.to(torch.float16), table[0], seq_len)
+    assert_close(got.float().cpu().numpy(), want_b, atol=8e-3, rtol=2e-2, what="bf16 query")
+
+
+def test_prefill_scale_is_a_parameter(gpu_ops):
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(12)
+    cache = Cache(10, lay)
+    table = random_tables(gen, [500], 10)
+    fill_sequence(gpu_ops, cache, gen, table[0], 500)
+    q = seeded_normal(gen, (40, 24, 128))
+    got = _run(cache, q, table[0], 500, scale=0.05).float().cpu().numpy()
+    assert_close(got, _oracle(cache, q, table[0], 500, scale=0.05), what="scale 0.05")
+
+
+def test_prefill_rejections(gpu_ops):
+    lay = PageLayout(4, 128)
+    cache = Cache(4, lay)
+    row = torch.arange(4, dtype=torch.int32)
+    q = torch.zeros(10, 24, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="query longer than the KV sequence"):
+        _run(cache, q, row, 9)
+    with pytest.raises(RuntimeError, match=r"query has 12 heads, the K8/V4 cache holds 4 \(needs 24\)"):
+        _run(cache, torch.zeros(10, 12, 128, dtype=torch.float16), row, 100)
+    with pytest.raises(RuntimeError, match="block table row covers 256 tokens"):
+        _run(cache, q, row, 300)
+    empty = torch.zeros(0, 24, 128, dtype=torch.float16, device=DEV)
+    assert hip_prefill(empty, cache.views, row.to(DEV), 5, 1, 0.1) is empty
+
+
+def test_prefill_chunk_4224_over_131072_sampled_rows(gpu_ops):
+    """The benchmark shape: a 4,224-token chunk after 131,072 cached tokens (24/4 heads, D=128).
+
+    The chunk's own K/V are written by the store kernel first; rows across the
+    chunk (first, last, both ends of work-group blocks) are checked against the
+    oracle over all 135,296 keys."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(1005)
+    seq_len, q_len = 131072 + 4224, 4224
+    pages = seq_len // PAGE
+    cache = Cache(pages + 16, lay)
+    table = random_tables(gen, [seq_len], pages + 16)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len)
+    q = seeded_normal(gen, (q_len, 24, 128))
+    got = _run(cache, q, table[0], seq_len).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rows = np.array([0, 1, 20, 21, 22, 1000, 2047, 3000, 4181, 4222, 4223])
+    want = _oracle(cache, q, table[0], seq_len, rows=rows)
+    err = assert_close(got[rows], want, what="4224x131072")
+    print("  sampled rows max abs err %.2e" % err, flush=True)
