@@ -407,7 +407,7 @@ def config_rows(torch, hip, ops, steps, warmup):
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
               "(got --gpus %d)" % args.gpus, file=sys.stderr)
         return 2
     import torch

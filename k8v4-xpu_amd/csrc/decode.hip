@@ -13,18 +13,22 @@
 //    all sequences are cut into runs of P pages that never straddle a
 //    sequence, so a batch of 4 x 128K and a batch of {2K, 32K, 128K, 200K}
 //    both fill the chip.  No host read of the lengths: graph-capturable.
-//  * A work-group is one wave per KV head.  The wave keeps the 6*q_len query
-//    rows of its head (padded to 16-row tiles) as int8 MFMA operands, so each
-//    K/V byte is fetched from HBM once and used for every GQA row.
-//  * Per 32-token chunk: QK^T on v_mfma_i32_16x16x64_i8 computed transposed
-//    (tokens x rows) so the score tile lands in the A-operand layout of the
-//    P.V MFMA; online softmax in the exp2 domain with a lazy rescale (the
-//    running max only moves when a row's max grows by more than 2^8); V
-//    nibbles expanded in registers to fp16 with a byte-permute + magic-number
-//    trick ((1024 + nibble) - (1024 + zero)) * scale; P.V and the row sums on
-//    v_mfma_f32_16x16x32_f16 with fp32 accumulation.
-//  * K, V and the scale planes of the next PF chunks are in flight in
-//    registers while the current chunk is computed (one wave per SIMD).
+//  * A work-group holds one or two waves per KV head.  Each wave keeps the
+//    6*q_len query rows of its head (int8-quantized in the prologue, padded to
+//    16-row tiles) as MFMA operands, so each K/V byte is fetched from HBM once
+//    and used for every GQA row.
+//  * Each wave owns a ring of LDS slots filled by direct-to-LDS loads
+//    (global_load_lds, nontemporal for K and V): one slot is one 32-token
+//    chunk of its head (K rows with XOR-swizzled 16-byte chunks, V rows in a
+//    rotated order, the three scale planes), so the next chunks stream in
+//    without holding registers and every operand read is conflict-free.
+//  * Per chunk: QK^T on v_mfma_i32_16x16x64_i8 computed transposed (tokens x
+//    rows) so the score tile lands in the operand layout of the P.V MFMA;
+//    online softmax in the exp2 domain with a lazy rescale; V nibbles are used
+//    as fp16 subnormal operands straight from the packed bytes (n * 2^-24 and
+//    16 n * 2^-24 after one AND), the V scale multiplies P and the zero point
+//    is one extra MFMA per tile (sum_t p_t s_t z_t), removed at the end;
+//    P.V and the row sums on v_mfma_f32_16x16x32_f16 with fp32 accumulation.
 //  * Each split writes (m, l, unnormalized O) for its live rows only; a small
 //    merge kernel combines the splits of each output row.
 #include "k8v4_common.h"

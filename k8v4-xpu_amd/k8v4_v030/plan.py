@@ -5,7 +5,7 @@ captured graph never reads them back from the device.
 
 Reference: k8v4_v030/plan.py:22-146.  Differences: the head dim is a parameter
 (128 or 256) instead of the fixed 256, and ``attn_workspace_bytes`` sizes the
-split-K scratch of this build's decode kernel.
+split-K scratch of the HIP decode kernel.
 """
 from __future__ import annotations
 

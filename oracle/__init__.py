@@ -24,5 +24,5 @@ How each part is pinned (tests/test_oracle.py): known-answer vectors in
 geometry constants), closed forms (a single key returns its value row, equal
 keys average the values), invariants (round-trip error bounds), and reduction
 to a library routine (torch's scaled_dot_product_attention on the dequantized
-tensors).  See the "Parity" section of DESIGN.md for the list.
+tensors); tests/test_oracle.py holds each check.
 """
