@@ -790,10 +790,12 @@ void decode_split_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------ merge kernel
-// One 256-thread work-group per output row (token, query head).  The splits
-// of the row are spread over the threads: thread t handles 16-byte column
-// t % (D/4) of splits s = t / (D/4) (mod 256 / (D/4)), four loads in flight,
-// then the partial sums are folded in LDS.
+// One 256-thread work-group per output row (token, query head).  Thread t
+// owns 16-byte column t % (D/4) of the row and the splits s = t / (D/4) +
+// k * (256 / (D/4)).  It loads the (m, l, O) of up to MU of its splits at once
+// and folds them online (running max, rescaled sums), so the whole merge is
+// one round trip to memory; the per-thread partial states are then combined
+// in LDS with the same rescaling.
 
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
   if (dtype == K8V4_F32)
@@ -807,7 +809,8 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   constexpr int VPR = D / 4;       // 16-byte columns per row state
-  constexpr int SPI = 256 / VPR;   // splits handled per pass
+  constexpr int SPI = 256 / VPR;   // split groups per work-group
+  constexpr int MU = 8;            // splits loaded together by one thread
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int hq = kGqa * a.hkv;
@@ -829,59 +832,65 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const int64_t l_off = m_off + a.hkv * rows;
   const float *ws = a.ws + static_cast<int64_t>(first) * a.split_floats;
 
-  __shared__ float red_m[4];
-  __shared__ v4f red_o[SPI][VPR];
+  __shared__ float red_m[SPI];
   __shared__ float red_l[SPI];
-
-  // Global max over the splits of this row.
-  float M = -INFINITY;
-  for (int s = tid; s < count; s += 256) M = fmaxf(M, ws[s * a.split_floats + m_off]);
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m, kWave));
-  if (lane == 0) red_m[tid / kWave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  __shared__ v4f red_o[SPI][VPR];
 
   const int col = tid % VPR, sg = tid / VPR;
+  float M = -INFINITY, lacc = 0.f;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  float lacc = 0.f;
-  if (M != -INFINITY) {
-    int s = sg;
-    for (; s + 3 * SPI < count; s += 4 * SPI) {
-      float ms[4], ls[4];
-      v4f os[4];
+  for (int s0 = sg; s0 < count; s0 += MU * SPI) {
+    float ms[MU], ls[MU];
+    v4f os[MU];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float *st = ws + static_cast<int64_t>(s + u * SPI) * a.split_floats;
-        ms[u] = st[m_off];
-        ls[u] = st[l_off];
-        os[u] = *reinterpret_cast<const v4f *>(st + o_off + 4 * col);
+    for (int u = 0; u < MU; ++u) {
+      const int s = s0 + u * SPI;
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
+      os[u] = (v4f){0.f, 0.f, 0.f, 0.f};
+      if (s < count) {
+        const float *st = ws + static_cast<int64_t>(s) * a.split_floats;
+        ms[u] = __builtin_nontemporal_load(st + m_off);
+        ls[u] = __builtin_nontemporal_load(st + l_off);
+        os[u] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(st + o_off + 4 * col));
       }
+    }
+    float mn = M;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - M);
+    for (int u = 0; u < MU; ++u) mn = fmaxf(mn, ms[u]);
+    if (mn != -INFINITY) {
+      const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
+      lacc *= c;
+      acc *= c;
+#pragma unroll
+      for (int u = 0; u < MU; ++u) {
+        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn);
         lacc += w * ls[u];
         acc += w * os[u];
       }
-    }
-    for (; s < count; s += SPI) {
-      const float *st = ws + static_cast<int64_t>(s) * a.split_floats;
-      const float ms = st[m_off];
-      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      lacc += w * st[l_off];
-      acc += w * *reinterpret_cast<const v4f *>(st + o_off + 4 * col);
+      M = mn;
     }
   }
   red_o[sg][col] = acc;
-  if (col == 0) red_l[sg] = lacc;
+  if (col == 0) {
+    red_m[sg] = M;
+    red_l[sg] = lacc;
+  }
   __syncthreads();
   if (tid >= VPR) return;
+  float Mg = -INFINITY;
+#pragma unroll
+  for (int g2 = 0; g2 < SPI; ++g2) Mg = fmaxf(Mg, red_m[g2]);
   float l = 0.f;
   v4f o = {0.f, 0.f, 0.f, 0.f};
+  if (Mg != -INFINITY) {
 #pragma unroll
-  for (int g2 = 0; g2 < SPI; ++g2) {
-    l += red_l[g2];
-    o += red_o[g2][tid];
+    for (int g2 = 0; g2 < SPI; ++g2) {
+      const float mg = red_m[g2];
+      const float w = mg == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg - Mg);
+      l += w * red_l[g2];
+      o += w * red_o[g2][tid];
+    }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * tid;

@@ -4,10 +4,12 @@
 // Reference: k8v4_v030/native/xe2_kv_ops.cpp:536-627 (two kernels, fp32
 // arithmetic with rint) and the parity oracle k8v4_v030/oracle.py:18-69
 // (float64, half-away-from-zero for K, floor(x+0.5) for V).  This kernel
-// follows the oracle: every rounding step is the same IEEE double operation
-// in the same order, so codes and stored scales are bit-identical to it.
-// This file is compiled with -ffp-contract=off and the kernel body disables
-// contraction as well, so no multiply-add is fused.
+// follows the oracle: scales are the same IEEE double operations in the same
+// order, and every code equals the float64 rule's (an fp32 evaluation is used
+// only where its error bound cannot change the result, see below), so codes
+// and stored scales are bit-identical to it.  This file is compiled with
+// -ffp-contract=off and the kernel body disables contraction as well, so no
+// multiply-add is fused.
 //
 // Mapping (MI355X): K and V of one (token, kv_head) pair are handled by the
 // same D/8 lanes, 8 consecutive dims per lane (one 16-byte load of K and one
@@ -106,16 +108,35 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   const int64_t row = slot - page * kPage;
   const int64_t cell = row * a.hkv + head;
 
+  // Codes are evaluated in fp32 first.  The fp32 value of each pre-rounding
+  // quantity is within 2e-5 of the float64 one the rule defines (|y| <= 127
+  // for K; |x / s| <= 16.5 wherever the V code is not clamped), so its floor is
+  // the float64 floor unless it lies within 2^-12 of an integer; those
+  // elements (ties such as x = amax / 254, constant rows) take the float64
+  // path, step for step as the rule is written.
+  constexpr float kMargin = 0x1p-12f;
+
   // K: symmetric int8, scale amax/127, round half away from zero.
   const double k_scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
   uint32_t kw[2] = {0u, 0u};
   if (amax != 0.f) {
     const double inv = 1.0 / k_scale;
+    const float inv32 = static_cast<float>(inv);
+    const bool fast = inv32 <= 3.0e38f;  // a tiny bf16 amax overflows the fp32 reciprocal
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const double y = static_cast<double>(kx[i]) * inv;
-      double q = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
-      q = fmin(fmax(q, -127.0), 127.0);
+      const float y32 = kx[i] * inv32;
+      const float d = fabsf(y32) + 0.5f;
+      float m = floorf(d);
+      const float fr = d - m;
+      float q;
+      if (!fast || fr < kMargin || fr > 1.f - kMargin) {
+        const double y = static_cast<double>(kx[i]) * inv;
+        q = static_cast<float>(y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5));
+      } else {
+        q = y32 >= 0.f ? m : -m;
+      }
+      q = fminf(fmaxf(q, -127.f), 127.f);
       const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(q)) & 0xFFu;
       kw[i >> 2] |= b << (8 * (i & 3));
     }
@@ -126,11 +147,17 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   const double span = (hi_d - lo_d) / 15.0;
   const double v_scale = span >= 1.0e-8 ? span : 1.0e-8;
   const double zero = fmin(fmax(floor(-lo_d / v_scale + 0.5), 0.0), 15.0);
+  const float rs32 = static_cast<float>(1.0 / v_scale);
+  const float z32 = static_cast<float>(zero);
   uint32_t vw = 0u;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    double q = floor(static_cast<double>(vx[i]) / v_scale + zero + 0.5);
-    q = fmin(fmax(q, 0.0), 15.0);
+    const float y32 = vx[i] * rs32 + z32 + 0.5f;
+    float q = floorf(y32);
+    const float fr = y32 - q;
+    if (fr < kMargin || fr > 1.f - kMargin)
+      q = static_cast<float>(floor(static_cast<double>(vx[i]) / v_scale + zero + 0.5));
+    q = fminf(fmaxf(q, 0.f), 15.f);
     vw |= static_cast<uint32_t>(q) << (4 * i);
   }
 

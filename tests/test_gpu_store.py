@@ -184,3 +184,41 @@ def test_bound_store_matches_the_plain_op(gpu_ops):
     assert np.array_equal(b.view(torch.uint8).cpu().numpy(), _oracle_blob(20, geom, k, v, slots))
     assert gpu_ops.bind_kv_store_paged(k[:0].to(DEV), v[:0].to(DEV), slots[:0].to(DEV), vb["k"], vb["k_scale"],
                                        vb["v"], vb["v_scale"], vb["v_zero"]) is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_store_extreme_magnitudes_and_rounding_ties(gpu_ops, dtype):
+    """Rows that stress every shortcut of the code evaluation, byte-compared with the oracle:
+    tiny and huge magnitudes (bf16 subnormals, 1e37), constant rows, exact K ties
+    (x = amax * (2k+1) / 254) and V values on rounding boundaries."""
+    d, hkv = 128, 4
+    layout = PageLayout(hkv, d)
+    geom = paged.Geometry(hkv, d)
+    g = torch.Generator().manual_seed(91)
+    base = torch.randn(64, hkv, d, generator=g)
+    rows_k, rows_v = [], []
+    mags = [1e-40, 1e-38, 3e-5, 1.0, 300.0, 1e4] + ([1e20, 1e37] if dtype == torch.bfloat16 else [])
+    for m in mags:
+        rows_k.append(base[len(rows_k) % 64] * m)
+        rows_v.append(base[(len(rows_v) + 7) % 64] * m)
+    # exact half-way K codes: amax = 1, entries (2k+1)/254
+    tie = torch.tensor([(2 * k + 1) / 254.0 for k in range(d)]).clamp(max=1.0)
+    tie[0] = 1.0
+    rows_k.append(tie.expand(hkv, d).clone())
+    rows_v.append(torch.linspace(-1, 1, d).expand(hkv, d).clone())
+    # constant rows and a V row whose values sit on code boundaries
+    rows_k.append(torch.full((hkv, d), 0.25))
+    rows_v.append(torch.full((hkv, d), -3.0))
+    span = torch.arange(d, dtype=torch.float32) % 16 / 15.0 * 2 - 1
+    rows_k.append(torch.zeros(hkv, d))
+    rows_v.append((span + 1 / 30.0).expand(hkv, d).clone())
+    k = torch.stack(rows_k).to(dtype)
+    v = torch.stack(rows_v).to(dtype)
+    n = k.shape[0]
+    slots = torch.arange(n, dtype=torch.int64) * 5
+    raw, views = _cache(4, layout)
+    _store(gpu_ops, views, k.to(DEV), v.to(DEV), slots.to(DEV))
+    torch.cuda.synchronize()
+    want = _oracle_blob(4, geom, k, v, slots)
+    got = raw.cpu().numpy()
+    assert np.array_equal(got, want), "bytes differ at %s" % np.nonzero(got != want)[0][:10]
