@@ -194,14 +194,15 @@ struct Slot {
   static constexpr int KS = D / 64;     // 64-dim k-steps of the QK MFMA
   static constexpr int DG = D / 128;    // 8-dim dword groups per lane in a V row
   static constexpr int VROW = D / 2;    // bytes of one token's V row (one head)
-  static constexpr int K_OFF = 0;       // [32 tokens][D] rows, 16-byte chunks XOR-swizzled per row
   static constexpr int KRP = 1024 / D;  // K rows per 1 KB DMA
-  static constexpr int V_OFF = 32 * D;  // [32 tokens][VROW]: V rows as stored
-  static constexpr int S_OFF = V_OFF + 32 * VROW;  // ks[32] | vs[32] | vz[32] | vz[32] floats
-  static constexpr int BYTES = S_OFF + 512;
-  static constexpr int NV = 32 * VROW / 1024;       // 16-byte DMAs for the V rows
-  static constexpr int NK = 32 * D / 1024;          // 16-byte DMAs for the K rows
-  static constexpr int NDMA = NK + NV + 2;          // DMA instructions per chunk
+  // K slot: [32 tokens][D] codes, 16-byte chunks XOR-swizzled per row.
+  static constexpr int K_BYTES = 32 * D;
+  // V slot: [32 tokens][VROW] V rows (rotated order), then ks[32] | vs[32] | vz[32].
+  static constexpr int S_OFF = 32 * VROW;
+  static constexpr int V_BYTES = S_OFF + 384;
+  static constexpr int NK = 32 * D / 1024;       // 16-byte DMAs for the K rows
+  static constexpr int NV = 32 * VROW / 1024;    // 16-byte DMAs for the V rows
+  static constexpr int NVS = NV + 2;             // V rows + the two scale-plane DMAs
 };
 
 // K rows sit in LDS with their 16-byte chunks permuted: chunk c of row t is at
@@ -275,53 +276,71 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int h, int n, int g, int lan
 // the scale planes of this head are gathered with two 4-byte DMAs (lanes
 // 0-31: k_scale then v_zero, lanes 32-63: v_scale then v_zero again).
 template <int D, int HKV>
-__device__ __forceinline__ int issue_chunk(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
-                                           int lane, lds_t *slot) {
+__device__ __forceinline__ int issue_k(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
+                                       lds_t *kslot) {
   using S = Slot<D>;
   const int p = x >> 1, half = x & 1;
   int phys = physical_page(a, bt_row, p);
   const int valid = (phys >= 0 && phys < a.num_pages) ? 1 : 0;
   if (!valid) phys = 0;
-  const int tok0 = 32 * half;
-  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + static_cast<int64_t>(tok0) * HKV * D;
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps +
+                   static_cast<int64_t>(32 * half) * HKV * D;
 #pragma unroll
   for (int j = 0; j < S::NK; ++j)
-    dma16_nt(kb + static_cast<int64_t>(j) * S::KRP * (HKV * D) + lo.k[j & 3], slot + S::K_OFF + j * 1024);
+    dma16_nt(kb + static_cast<int64_t>(j) * S::KRP * (HKV * D) + lo.k[j & 3], kslot + j * 1024);
+  return valid;
+}
+
+template <int D, int HKV>
+__device__ __forceinline__ void issue_v(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
+                                        int lane, lds_t *vslot) {
+  using S = Slot<D>;
+  const int p = x >> 1, half = x & 1;
+  int phys = physical_page(a, bt_row, p);
+  if (phys < 0 || phys >= a.num_pages) phys = 0;
+  const int tok0 = 32 * half;
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps +
                    static_cast<int64_t>(tok0) * HKV * S::VROW;
 #pragma unroll
   for (int j = 0; j < S::NV; ++j)
-    dma16_nt(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, slot + S::V_OFF + j * 1024);
+    dma16_nt(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, vslot + j * 1024);
   const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4 + lo.s;
   const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0;
   const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0;
   const char *vzp = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + plane0;
-  dma4(lane < 32 ? ksp : vsp, slot + S::S_OFF);
-  dma4(vzp, slot + S::S_OFF + 256);
-  return valid;
+  dma4(lane < 32 ? ksp : vsp, vslot + S::S_OFF);        // ks[32] | vs[32]
+  if (lane < 32) dma4(vzp, vslot + S::S_OFF + 256);     // vz[32]
 }
 
 // Wait until at most `after` chunks' DMAs are still in flight.
-template <int NDMA>
-__device__ __forceinline__ void wait_chunks(int after) {
-  static_assert(2 * NDMA <= 63, "vmcnt holds at most 63 outstanding loads");
-  if (after >= 2)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
-  else if (after == 1)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Wait until at most n (wave-uniform, 0..) vector-memory loads are
+// outstanding.  s_waitcnt takes an immediate, so the count is dispatched;
+// counts above 62 wait for 62 (more than needed, still correct).
+__device__ __forceinline__ void wait_vm(int n) {
+#define K8V4_WAIT_CASE(N) \
+  case N:                 \
+    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
+    break;
+  switch (n < 62 ? n : 62) {
+    K8V4_WAIT_CASE(0) K8V4_WAIT_CASE(1) K8V4_WAIT_CASE(2) K8V4_WAIT_CASE(3) K8V4_WAIT_CASE(4)
+    K8V4_WAIT_CASE(5) K8V4_WAIT_CASE(6) K8V4_WAIT_CASE(7) K8V4_WAIT_CASE(8) K8V4_WAIT_CASE(9)
+    K8V4_WAIT_CASE(10) K8V4_WAIT_CASE(11) K8V4_WAIT_CASE(12) K8V4_WAIT_CASE(13) K8V4_WAIT_CASE(14)
+    K8V4_WAIT_CASE(15) K8V4_WAIT_CASE(16) K8V4_WAIT_CASE(17) K8V4_WAIT_CASE(18) K8V4_WAIT_CASE(19)
+    K8V4_WAIT_CASE(20) K8V4_WAIT_CASE(21) K8V4_WAIT_CASE(22) K8V4_WAIT_CASE(23) K8V4_WAIT_CASE(24)
+    K8V4_WAIT_CASE(25) K8V4_WAIT_CASE(26) K8V4_WAIT_CASE(27) K8V4_WAIT_CASE(28) K8V4_WAIT_CASE(29)
+    K8V4_WAIT_CASE(30) K8V4_WAIT_CASE(31) K8V4_WAIT_CASE(32) K8V4_WAIT_CASE(33) K8V4_WAIT_CASE(34)
+    K8V4_WAIT_CASE(35) K8V4_WAIT_CASE(36) K8V4_WAIT_CASE(37) K8V4_WAIT_CASE(38) K8V4_WAIT_CASE(39)
+    K8V4_WAIT_CASE(40) K8V4_WAIT_CASE(41) K8V4_WAIT_CASE(42) K8V4_WAIT_CASE(43) K8V4_WAIT_CASE(44)
+    K8V4_WAIT_CASE(45) K8V4_WAIT_CASE(46) K8V4_WAIT_CASE(47) K8V4_WAIT_CASE(48) K8V4_WAIT_CASE(49)
+    K8V4_WAIT_CASE(50) K8V4_WAIT_CASE(51) K8V4_WAIT_CASE(52) K8V4_WAIT_CASE(53) K8V4_WAIT_CASE(54)
+    K8V4_WAIT_CASE(55) K8V4_WAIT_CASE(56) K8V4_WAIT_CASE(57) K8V4_WAIT_CASE(58) K8V4_WAIT_CASE(59)
+    K8V4_WAIT_CASE(60) K8V4_WAIT_CASE(61)
+    default:
+      asm volatile("s_waitcnt vmcnt(62)" ::: "memory");
+      break;
+  }
+#undef K8V4_WAIT_CASE
 }
-
-// (x & mask) | bits in one v_and_or_b32 (the compiler otherwise emits an AND
-// and an OR with literal operands).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
-  return r;
-}
-constexpr uint32_t kNibMask = 0x000F000Fu;  // low nibble of each 16-bit half
-constexpr uint32_t kMagic = 0x64006400u;    // fp16 1024.0 in both halves
 
 __device__ __forceinline__ v2h pack_h2(float lo, float hi) {
   return __builtin_convertvector((v2f){lo, hi}, v2h);
@@ -348,10 +367,10 @@ struct WaveState {
 };
 
 template <int D, int NT, bool QLDS>
-__device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const lds_t *slot, const lds_t *qlds,
-                                              int tbase, int L0, int lane, int g, bool masked) {
+__device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const lds_t *kslot, const lds_t *qlds,
+                                         int lane, int g, v4i (&sc)[2][NT]) {
   using S = Slot<D>;
-  constexpr int KS = S::KS, DG = S::DG;
+  constexpr int KS = S::KS;
   // ---- QK^T, transposed: S[ml][nt] lane (n,g) reg i = score(token 16*ml+4g+i, row 16*nt+n)
   v4i kf[2][KS];
   const int n = lane & 15;
@@ -361,9 +380,8 @@ __device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const 
     for (int ks = 0; ks < KS; ++ks) {
       const int t = 16 * ml + n, c = 4 * ks + g;
       kf[ml][ks] = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
-          slot + S::K_OFF + t * D + 16 * (c ^ kswz<D>(t)));
+          kslot + t * D + 16 * (c ^ kswz<D>(t)));
     }
-  v4i sc[2][NT];
 #pragma unroll
   for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
@@ -380,12 +398,22 @@ __device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const 
       }
       sc[ml][nt] = acc;
     }
+}
+
+// Softmax and P.V of one chunk whose scores chunk_qk produced; reads the V
+// rows and scale planes of the chunk's V slot.
+template <int D, int NT, bool QLDS>
+__device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, const v4i (&sc)[2][NT],
+                                                 const lds_t *vslot, int tbase, int L0, int lane, int g,
+                                                 bool masked) {
+  using S = Slot<D>;
+  constexpr int DG = S::DG;
   // Phase fences keep the scheduler from hoisting later LDS reads into this
   // phase, which would raise register pressure past two waves per SIMD.
   __builtin_amdgcn_sched_barrier(0);
   // ---- scale planes of this lane's 8 tokens: [0..3] = tokens 4g+i, [4..7] = 16+4g+i
   typedef float v4f_l __attribute__((ext_vector_type(4)));
-  const auto *sp = reinterpret_cast<const __attribute__((address_space(3))) v4f_l *>(slot + S::S_OFF);
+  const auto *sp = reinterpret_cast<const __attribute__((address_space(3))) v4f_l *>(vslot + S::S_OFF);
   v4f_l ksa = sp[g], ksb = sp[4 + g], vsa = sp[8 + g], vsb = sp[12 + g], vza = sp[16 + g], vzb = sp[20 + g];
   float ksv[8] = {ksa[0], ksa[1], ksa[2], ksa[3], ksb[0], ksb[1], ksb[2], ksb[3]};
   float vsv[8] = {vsa[0], vsa[1], vsa[2], vsa[3], vsb[0], vsb[1], vsb[2], vsb[3]};
@@ -477,17 +505,18 @@ __device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const 
     st.corr[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], bz, st.corr[nt], 0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // ---- V: the nibble bits themselves are the B operand, read as fp16
-  // subnormals: (x & 0x000F000F) is q * 2^-24 for the even dim of a byte and
-  // (x & 0x00F000F0) is q * 2^-20 for the odd dim.  Exact; the finalization
-  // rescales by 2^24 / 2^20 and subtracts the zero-point correction.
+  // ---- V: the packed bytes themselves are the B operand, read as fp16
+  // subnormals: a byte in the low half of a 16-bit lane is (16 hi + lo) * 2^-24
+  // and (x & 0x00F000F0) is hi * 2^-20.  Exact; the finalization takes the
+  // even dim as the difference, rescales by 2^24 / 2^20 and subtracts the
+  // zero-point correction.
 #pragma unroll
   for (int dg = 0; dg < DG; ++dg) {
     uint32_t vw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       vw[i] = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
-          slot + S::V_OFF + vrow_pos<D>(g, i) * S::VROW + 64 * dg + 4 * (lane & 15));
+          vslot + vrow_pos<D>(g, i) * S::VROW + 64 * dg + 4 * (lane & 15));
 #pragma unroll
     for (int byte = 0; byte < 4; ++byte) {
       const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + byte) << 16) | static_cast<uint32_t>(byte);
@@ -495,7 +524,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<D, NT, QLDS> &st, const 
 #pragma unroll
       for (int qp = 0; qp < 4; ++qp) {
         const uint32_t xw = __builtin_amdgcn_perm(vw[2 * qp + 1], vw[2 * qp], sel);
-        be[qp] = xw & 0x000F000Fu;
+        be[qp] = xw;
         bo[qp] = xw & 0x00F000F0u;
       }
       const v8h Be = __builtin_bit_cast(v8h, (v4i){static_cast<int>(be[0]), static_cast<int>(be[1]),
@@ -522,30 +551,44 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
 #pragma unroll
     for (int dg = 0; dg < D / 128; ++dg)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float sc = (j & 1) ? 1048576.0f : 16777216.0f;
+      for (int j = 0; j < 8; j += 2) {
+        // O[j] holds sum p' (16 hi + lo) 2^-24 (the whole byte), O[j+1] holds
+        // sum p' 16 hi 2^-24: the even dim is their difference.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st.O[nt][dg][j][i] = fmaf(st.O[nt][dg][j][i], sc, -st.corr[nt][i]);
+        for (int i = 0; i < 4; ++i) {
+          const float whole = st.O[nt][dg][j][i], high = st.O[nt][dg][j + 1][i];
+          st.O[nt][dg][j][i] = fmaf(whole - high, 16777216.0f, -st.corr[nt][i]);
+          st.O[nt][dg][j + 1][i] = fmaf(high, 1048576.0f, -st.corr[nt][i]);
+        }
       }
 }
 
 template <int D, int NT, int HKV, int NWH>
 struct SplitConfig {
-  // Two waves per head keep the int8 Q operands in LDS (shared by the pair)
-  // and a 2-slot ring per wave; one wave per head keeps Q in registers and a
-  // 3-slot ring.
+  // Two waves per head keep the int8 Q operands in LDS (shared by the pair);
+  // one wave per head keeps Q in registers.  Each wave owns a K ring of RK
+  // slots and a V ring of RV slots, as deep as the LDS allows: a K slot is
+  // refilled as soon as its QK^T product is issued, so while a wave computes
+  // one chunk up to RK - 1 K slots and RV - 1 V slots are in flight.
   static constexpr bool QLDS = NWH > 1;
-  static constexpr int R = QLDS ? 2 : 3;  // LDS ring slots per wave
   static constexpr int WAVES = HKV * NWH;
   static constexpr int Q_FRAG_BYTES = NT * (D / 64) * kWave * 16;         // int8 B-operand fragments
   static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_FRAG_BYTES + NT * 16 * 4 : 0;  // + per-row factors
-  static constexpr int Q_OFF = WAVES * R * Slot<D>::BYTES;
+  static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
+  // 4 / HKV work-groups share a CU (the grid is about that many per CU).
+  static constexpr int LDS_MAX = 163840 * HKV / 4;
+  static constexpr int RV = 2;
+  static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
+  static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
+  static constexpr int WAVE_BYTES = RK * Slot<D>::K_BYTES + RV * Slot<D>::V_BYTES;
+  static constexpr int Q_OFF = WAVES * WAVE_BYTES;
   static constexpr int RING_BYTES = Q_OFF + HKV * Q_BYTES_PER_HEAD;
   // Partner-wave state exchange at the end (reuses the ring memory).
   static constexpr int XCHG_FLOATS = (NT * (D / 128) * 8 * 4 + NT * 4 + NT) * kWave;
   static constexpr int XCHG_BYTES = NWH > 1 ? HKV * XCHG_FLOATS * 4 : 0;
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
   static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
+  static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
 };
 
 template <int D, int NT, int HKV, int NWH>
@@ -554,7 +597,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV * NWH, 64 * HKV *
 void decode_split_kernel(DecodeArgs a) {
   using S = Slot<D>;
   using CFG = SplitConfig<D, NT, HKV, NWH>;
-  constexpr int KS = S::KS, DG = S::DG, R = CFG::R;
+  constexpr int KS = S::KS, DG = S::DG, RK = CFG::RK, RV = CFG::RV;
   __shared__ __attribute__((aligned(16))) char lds_raw[CFG::LDS_BYTES];
   lds_t *lds = (lds_t *)(lds_raw);
 
@@ -582,11 +625,29 @@ void decode_split_kernel(DecodeArgs a) {
   // This wave's chunks: x0 + w + k*NWH for k < cnt.
   const int my0 = x0 + w;
   const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
-  lds_t *ring = lds + wave * R * S::BYTES;
+  lds_t *kring = lds + wave * CFG::WAVE_BYTES;
+  lds_t *vring = kring + RK * S::K_BYTES;
   const LaneOffsets lo = lane_offsets<D, HKV>(h, n, g, lane);
-  uint32_t valid_mask = 0;  // bit s: ring slot s holds a chunk of a valid page
-  for (int s = 0; s < R && s < cnt; ++s)
-    valid_mask |= static_cast<uint32_t>(issue_chunk<D, HKV>(a, bt_row, my0 + s * NWH, lo, lane, ring + s * S::BYTES)) << s;
+  // DMA bookkeeping (wave-uniform): `issued` counts this wave's DMA
+  // instructions; mk[s] / mv[s] is the count right after the K / V group of
+  // ring slot s was issued, so a chunk is resident once at most
+  // issued - max(mk, mv) loads remain outstanding (loads complete in order).
+  int issued = 0;
+  int mk[4] = {0, 0, 0, 0}, mv[2] = {0, 0};
+  uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
+#pragma unroll
+  for (int s = 0; s < RK; ++s) {
+    if (s < cnt) {
+      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + s * NWH, lo, kring + s * S::K_BYTES)) << s;
+      issued += S::NK;
+      mk[s] = issued;
+      if (s < RV) {
+        issue_v<D, HKV>(a, bt_row, my0 + s * NWH, lo, lane, vring + s * S::V_BYTES);
+        issued += S::NVS;
+        mv[s] = issued;
+      }
+    }
+  }
 
   WaveState<D, NT, CFG::QLDS> st;
   lds_t *qlds = lds + CFG::Q_OFF + h * CFG::Q_BYTES_PER_HEAD;
@@ -697,18 +758,35 @@ void decode_split_kernel(DecodeArgs a) {
   }
 
   for (int k = 0; k < cnt; ++k) {
-    const int s = k % R;  // wave-uniform ring slot
-    lds_t *slot = ring + s * S::BYTES;
-    wait_chunks<S::NDMA>(min(R - 1, cnt - 1 - k));
-    if ((valid_mask >> s) & 1u) {
-      const int tbase = 32 * (my0 + k * NWH);
-      compute_chunk<D, NT, CFG::QLDS>(st, slot, qlds, tbase, L0, lane, g, tbase + 32 > min_end);
-    }
-    if (k + R < cnt) {
-      // The slot's LDS reads above have completed (their values fed the MFMAs).
+    const int sk = k % RK, sv = k % RV;  // wave-uniform ring slots
+    lds_t *kslot = kring + sk * S::K_BYTES;
+    lds_t *vslot = vring + sv * S::V_BYTES;
+    int mks = mk[0], mvs = mv[0];
+#pragma unroll
+    for (int s = 1; s < RK; ++s)
+      if (sk == s) mks = mk[s];
+    if (sv == 1) mvs = mv[1];
+    wait_vm(issued - max(mks, mvs));
+    const bool valid = (valid_mask >> sk) & 1u;
+    const int tbase = 32 * (my0 + k * NWH);
+    v4i sc[2][NT];
+    if (valid) chunk_qk<D, NT, CFG::QLDS>(st, kslot, qlds, lane, g, sc);
+    if (k + RK < cnt) {
+      // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const uint32_t v = static_cast<uint32_t>(issue_chunk<D, HKV>(a, bt_row, my0 + (k + R) * NWH, lo, lane, slot));
-      valid_mask = (valid_mask & ~(1u << s)) | (v << s);
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + (k + RK) * NWH, lo, kslot));
+      valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
+      issued += S::NK;
+#pragma unroll
+      for (int s = 0; s < RK; ++s)
+        if (sk == s) mk[s] = issued;
+    }
+    if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+    if (k + RV < cnt) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_v<D, HKV>(a, bt_row, my0 + (k + RV) * NWH, lo, lane, vslot);
+      issued += S::NVS;
+      if (sv == 0) mv[0] = issued; else mv[1] = issued;
     }
   }
 
