@@ -134,6 +134,10 @@ int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
  * fp32 accumulation.
  * out: [q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride
  *      (multiple of 4, base 16-byte aligned).
+ * workspace: caller-owned device scratch (16-byte aligned) of workspace_bytes
+ *      >= k8v4_prefill_workspace_bytes(seq_len, q_len, hkv, head_dim): partial
+ *      softmax states of the row blocks the balanced schedule splits between
+ *      work-groups.
  * q_len == 0 is a no-op; q_len > seq_len is an error.
  */
 int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
@@ -142,7 +146,13 @@ int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const i
                        int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
                        int64_t vz_page_stride, const int32_t *block_row, int64_t table_width,
                        int pages_per_block, int64_t seq_len, int64_t q_len, int hkv, int head_dim,
-                       float scale, void *out, int out_dtype, int64_t out_tok_stride, void *stream);
+                       float scale, void *out, int out_dtype, int64_t out_tok_stride,
+                       void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes k8v4_prefill_paged needs (0 for q_len == 0, -1 on bad
+ * arguments).  No counterpart in the reference (its prefill allocated its
+ * gathered K/V per head inside the call, onednn_prefill.py:226-239). */
+int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, int hkv, int head_dim);
 
 /* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
  * No counterpart in the reference (its caller sized [nprog, 64, D] fp32

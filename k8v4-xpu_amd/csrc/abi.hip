@@ -25,6 +25,19 @@ int launch_status(const char *what) {
   return K8V4_OK;
 }
 
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 }  // namespace k8v4
 
 extern "C" int k8v4_abi_version(void) { return K8V4_ABI_VERSION; }

@@ -31,6 +31,9 @@ void clear_error();
 // Checks the launch that was just enqueued.
 int launch_status(const char *what);
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cus();
+
 inline bool supported_heads(int hkv) { return hkv == 2 || hkv == 4; }
 inline bool supported_dim(int d) { return d == 128 || d == 256; }
 

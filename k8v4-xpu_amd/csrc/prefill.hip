@@ -22,17 +22,21 @@
 //    16 n * 2^-24 for odd dims) in a transposed tile, the V scale multiplies
 //    P and the zero point is subtracted once per row at the end:
 //      sum_t p_t (n_t - z_t) s_t = sum_t (p_t s_t) n_t - sum_t (p_t s_t) z_t.
-//  * S^T = K Q^T and O^T = V^T P'^T on v_mfma_f32_16x16x32_f16: the query row
-//    is the MFMA column, so each lane owns one row's softmax state and the
+//  * S^T = K Q^T and O^T = V^T P'^T on v_mfma_f32_32x32x16_f16 (the 32x32
+//    shapes run at twice the rate of the 16x16 ones on gfx950): the query row
+//    is the MFMA column, so a lane pair owns one row's softmax state and the
 //    score tile is already the B operand of the PV product.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
 //    only moves when a row's max grows by more than 2^8).
 #include "k8v4_common.h"
 
+#include <algorithm>
+
 namespace k8v4 {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -59,8 +63,12 @@ struct PrefillArgs {
   int q_len;
   int hkv;
   float c;       // softmax scale * log2(e)
-  int blocks;    // row blocks per KV head
-  int per_xcd;   // row blocks interleaved per XCD group (0: plain order)
+  int nbh;       // 128-row blocks per KV head
+  int tper;      // page steps of one head: sum over its blocks of the pages each reads
+  int total;     // page steps of the call (hkv * tper)
+  int grid;      // persistent work-groups; work-group v takes steps [v*total/grid, (v+1)*total/grid)
+  int xcd_perm;  // map ids so the work-groups of one XCD take adjacent work (grid % 8 == 0)
+  float *ws;     // partial states: [grid][2][128 rows][D + 2] floats
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -68,11 +76,10 @@ struct PrefillArgs {
 
 template <int D>
 struct Tile {
-  static constexpr int RT = D == 128 ? 2 : 1;        // 16-row MFMA tiles per wave
   static constexpr int WPE = D == 128 ? 2 : 1;       // waves per SIMD (LDS: one group per CU at D=256)
-  static constexpr int ROWS = 4 * 16 * RT;           // query rows per work-group
-  static constexpr int DS = D / 32;                  // k-steps of the QK MFMA
-  static constexpr int DT = D / 16;                  // 16-dim output tiles
+  static constexpr int ROWS = 4 * 32;                // query rows per work-group (one 32-row tile per wave)
+  static constexpr int DS = D / 16;                  // k-steps of the QK MFMA (16 dims each)
+  static constexpr int DT = D / 32;                  // 32-dim output tiles
   // MFMA tile of one page (one ring buffer).  Row paddings, not XOR
   // swizzles, keep the operand reads conflict-free, so every read address is
   // one per-lane base plus a compile-time offset.
@@ -211,19 +218,6 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
   }
 }
 
-__device__ __forceinline__ float xlane_max16_32(float x) {
-  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-}
-__device__ __forceinline__ float xlane_sum16_32(float x) {
-  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-}
-
 __device__ __forceinline__ void store_out4(void *out, int dtype, int64_t idx, v4f v) {
   if (dtype == K8V4_F32) {
     *reinterpret_cast<v4f *>(static_cast<float *>(out) + idx) = v;
@@ -237,214 +231,387 @@ __device__ __forceinline__ void store_out4(void *out, int dtype, int64_t idx, v4
   }
 }
 
+// ---- balanced schedule (shared by the attention and merge kernels)
+// The work of KV head h, row block rb is `block_pages(rb)` page steps; the
+// blocks are laid out head-major as one line of `total` steps, and the
+// persistent work-group v takes steps [v*total/grid, (v+1)*total/grid).  A
+// block split between work-groups is finished by the merge kernel from the
+// partial states the pieces leave in the workspace: the piece of work-group v
+// goes to slot 0 if v's range starts inside the block, else to slot 1.
+
+__device__ __forceinline__ int block_pages(const PrefillArgs &a, int rb) {
+  const int tok_hi = min(a.q_len - 1, (rb * 128 + 127) / 6);
+  return (a.seq_len - a.q_len + tok_hi + 1 + 63) / 64;
+}
+
+// Block of one head that contains step sp (0 <= sp < tper), and the steps of
+// the blocks before it.  Wave-uniform.
+__device__ __forceinline__ void locate_block(const PrefillArgs &a, int sp, int lane, int &rb, int &before) {
+  int base = 0;
+  rb = a.nbh - 1;
+  before = 0;
+  for (int r0 = 0; r0 < a.nbh; r0 += 64) {
+    const int r = r0 + lane;
+    const int n = r < a.nbh ? block_pages(a, r) : 0;
+    int incl = n;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    const uint64_t hit = __ballot(r < a.nbh && base + incl > sp);
+    if (hit) {
+      const int L = __builtin_ctzll(hit);
+      rb = __builtin_amdgcn_readfirstlane(r0 + L);
+      before = __builtin_amdgcn_readfirstlane(base + __shfl(incl - n, L, 64));
+      return;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+}
+
+__device__ __forceinline__ int range_start(const PrefillArgs &a, int v) {
+  return static_cast<int>(static_cast<int64_t>(v) * a.total / a.grid);
+}
+// Work-group whose range holds step s.
+__device__ __forceinline__ int range_owner(const PrefillArgs &a, int s) {
+  return static_cast<int>(((static_cast<int64_t>(s) + 1) * a.grid - 1) / a.total);
+}
+
+// One segment: pages [p_lo, p_hi) of row block rb of KV head h.  `part` is
+// null when the segment is the whole block (the output is written directly).
 template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
-prefill_kernel(PrefillArgs a) {
+__device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, int h, int rb, int p_lo, int p_hi,
+                                            float *part, int tid, int wave, int lane) {
   using T = Tile<D>;
-  constexpr int RT = T::RT;
-  __shared__ __attribute__((aligned(16))) char smem[2 * T::BUF + T::STAGE];
   lds_t *stage_lds = (lds_t *)(smem + 2 * T::BUF);
   const char *stage = smem + 2 * T::BUF;
-
-  // Work-group -> (KV head, row block).  With per_xcd > 0 the ids that land
-  // on one XCD (id % 8) all belong to one KV head, so its L2 holds one stream.
-  int h, rb;
-  const int id = blockIdx.x;
-  if (a.per_xcd > 0) {
-    h = (id % 8) / a.per_xcd;
-    rb = (id / 8) * a.per_xcd + (id % 8) % a.per_xcd;
-  } else {
-    h = id / a.blocks;
-    rb = id % a.blocks;
-  }
-  if (h >= a.hkv || rb >= a.blocks) return;
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-  const int lane = tid % 64, g = lane / 16, r16 = lane % 16;
   const int nrows = a.q_len * 6;
   const int row0 = rb * T::ROWS;
 
-  // ---- query fragments (B operand of S^T = K Q^T) and row limits
-  v8h qf[RT][T::DS];
-  int lim[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = row0 + wave * 16 * RT + rt * 16 + r16;
-    const bool valid = row < nrows;
-    const int tok = valid ? row / 6 : 0;
-    const int qh = h * 6 + (valid ? row % 6 : 0);
+  // ---- query fragments (B operand of S^T = K Q^T) and the row limit.
+  // Lane (r, hh): query row r = lane % 32 of the wave's tile, dims 16*ds + 8*hh.
+  const int hh = lane / 32, r32 = lane % 32;
+  const int row = row0 + wave * 32 + r32;
+  const bool row_valid = row < nrows;
+  v8h qf[T::DS];
+  int lim;
+  {
+    const int tok = row_valid ? row / 6 : 0;
+    const int qh = h * 6 + (row_valid ? row % 6 : 0);
     // A padding row sees key 0 only, which keeps its softmax finite.
-    lim[rt] = valid ? a.seq_len - a.q_len + tok + 1 : 1;
-    const uint16_t *src = a.q + static_cast<int64_t>(tok) * a.q_tok_stride + static_cast<int64_t>(qh) * D + 8 * g;
+    lim = row_valid ? a.seq_len - a.q_len + tok + 1 : 1;
+    const uint16_t *src = a.q + static_cast<int64_t>(tok) * a.q_tok_stride + static_cast<int64_t>(qh) * D + 8 * hh;
+    if (a.q_bf16) {
 #pragma unroll
-    for (int ds = 0; ds < T::DS; ++ds) {
-      const uint4 raw = valid ? *reinterpret_cast<const uint4 *>(src + 32 * ds) : make_uint4(0, 0, 0, 0);
-      if (a.q_bf16) {
+      for (int ds = 0; ds < T::DS; ++ds) {
+        const uint4 raw = row_valid ? *reinterpret_cast<const uint4 *>(src + 16 * ds) : make_uint4(0, 0, 0, 0);
         const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          qf[rt][ds][2 * e] = static_cast<_Float16>(__uint_as_float(w[e] << 16));
-          qf[rt][ds][2 * e + 1] = static_cast<_Float16>(__uint_as_float(w[e] & 0xFFFF0000u));
+          qf[ds][2 * e] = static_cast<_Float16>(__uint_as_float(w[e] << 16));
+          qf[ds][2 * e + 1] = static_cast<_Float16>(__uint_as_float(w[e] & 0xFFFF0000u));
         }
-      } else {
-        qf[rt][ds] = __builtin_bit_cast(v8h, raw);
+      }
+    } else {
+#pragma unroll
+      for (int ds = 0; ds < T::DS; ++ds) {
+        const uint4 raw = row_valid ? *reinterpret_cast<const uint4 *>(src + 16 * ds) : make_uint4(0, 0, 0, 0);
+        qf[ds] = __builtin_bit_cast(v8h, raw);
       }
     }
   }
 
-  // Keys this work-group needs, and the pages that need no causal mask.
+  // Pages that need no causal mask for any row of the block.
   const int tok_lo = row0 / 6;
-  const int tok_hi = min(a.q_len - 1, (row0 + T::ROWS - 1) / 6);
-  const int key_end = a.seq_len - a.q_len + tok_hi + 1;
-  const int npages = (key_end + 63) / 64;
   const int full_pages = (a.seq_len - a.q_len + tok_lo + 1) / 64;
 
-  v4f O[T::DT][RT];
-  float m_run[RT], lsum[RT], corr[RT];
+  v16f O[T::DT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    m_run[rt] = -INFINITY;
-    lsum[rt] = 0.f;
-    corr[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < T::DT; ++dt) O[dt][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
-  }
+  for (int dt = 0; dt < T::DT; ++dt) O[dt] = (v16f)0.f;
+  float m_run = -INFINITY, lsum = 0.f, corr = 0.f;
 
-  stage_page<D>(a, 0, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
+  // Per-lane LDS read bases.  K: key 32*mt + r32, dims 16*ds + 8*hh.  V^T:
+  // dim 32*dt + r32, key chunks c = 4*s + hh (+2) of the s-th 16-key step.
+  const int k_base = r32 * T::KROW + 16 * hh;
+  int v_off[8];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      v_off[2 * s + u] = vt_offset<D>(r32, 4 * s + 2 * u + hh);
+
+  stage_page<D>(a, p_lo, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
   wait_dma();
   __syncthreads();
-  convert_page<D>(a, 0, stage, smem, tid);
+  convert_page<D>(a, p_lo, stage, smem, tid);
   __syncthreads();
 
-  for (int p = 0; p < npages; ++p) {
-    const char *buf = smem + (p & 1) * T::BUF;
-    const bool more = p + 1 < npages;
-    if (more) stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + ((p + 1) & 1) * T::BUF + T::S_OFF));
+  for (int p = p_lo; p < p_hi; ++p) {
+    const int bi = (p - p_lo) & 1;
+    const char *buf = smem + bi * T::BUF;
+    const bool more = p + 1 < p_hi;
+    if (more) stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + (bi ^ 1) * T::BUF + T::S_OFF));
 
-    // ---- S^T = K Q^T for the 64 keys of page p
-    v4f S[4][RT];
+    // ---- S^T = K Q^T for the 64 keys of page p: lane (r, hh) reg 4j+i of
+    // tile mt holds key 32*mt + 8*j + 4*hh + i of row r.
+    v16f S[2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const char *krow = buf + (16 * kt + r16) * T::KROW;
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) S[kt][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < 2; ++mt) {
+      S[mt] = (v16f)0.f;
 #pragma unroll
       for (int ds = 0; ds < T::DS; ++ds) {
-        const v8h kf = *reinterpret_cast<const v8h *>(krow + (4 * ds + g) * 16);
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          S[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[rt][ds], S[kt][rt], 0, 0, 0);
+        const v8h kf = *reinterpret_cast<const v8h *>(buf + k_base + 32 * mt * T::KROW + 32 * ds);
+        S[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], S[mt], 0, 0, 0);
       }
     }
 
     // ---- scaled scores, masks, lazy max
     const float *sc = reinterpret_cast<const float *>(buf + T::S_OFF);
     const bool masked = p >= full_pages;
-    float mx[RT];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) mx[rt] = -INFINITY;
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const v4f ksc = *reinterpret_cast<const v4f *>(sc + 16 * kt + 4 * g);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+      for (int j = 0; j < 4; ++j) {
+        const int kb = 32 * mt + 8 * j + 4 * hh;
+        const v4f ksc = *reinterpret_cast<const v4f *>(sc + kb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float x = S[kt][rt][i] * ksc[i];
-          if (masked) {
-            const int key = p * 64 + 16 * kt + 4 * g + i;
-            x = key < lim[rt] ? x : -INFINITY;
-          }
-          S[kt][rt][i] = x;
-          mx[rt] = fmaxf(mx[rt], x);
+          float x = S[mt][4 * j + i] * ksc[i];
+          if (masked) x = p * 64 + kb + i < lim ? x : -INFINITY;
+          S[mt][4 * j + i] = x;
+          mx = fmaxf(mx, x);
         }
-    }
-    bool grow = false;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      mx[rt] = xlane_max16_32(mx[rt]);
-      grow |= mx[rt] > m_run[rt] + kThreshold;
-    }
-    if (__ballot(grow)) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const float mnew = fmaxf(m_run[rt], mx[rt]);
-        const float alpha = m_run[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rt] - mnew);
-        m_run[rt] = mnew;
-        lsum[rt] *= alpha;
-        corr[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < T::DT; ++dt) O[dt][rt] *= alpha;
       }
+    {
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    if (__ballot(mx > m_run + kThreshold)) {
+      const float mnew = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew);
+      m_run = mnew;
+      lsum *= alpha;
+      corr *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < T::DT; ++dt) O[dt] *= alpha;
     }
 
-    // ---- P' = exp2(x - m) * v_scale as the fp16 B operand; row sums and zero-point terms
-    v8h pb[2][RT];
+    // ---- P' = exp2(x - m) * v_scale as the fp16 B operand; row sums and zero-point terms.
+    // A row with no visible key yet (a segment that starts inside the causal
+    // tail) keeps m = -inf; its masked scores then give p = 0.
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    v8h pb[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const v4f vsc = *reinterpret_cast<const v4f *>(sc + 64 + 16 * kt + 4 * g);
-      const v4f vzc = *reinterpret_cast<const v4f *>(sc + 128 + 16 * kt + 4 * g);
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+      for (int j = 0; j < 4; ++j) {
+        const int kb = 32 * mt + 8 * j + 4 * hh;
+        const v4f vsc = *reinterpret_cast<const v4f *>(sc + 64 + kb);
+        const v4f vzc = *reinterpret_cast<const v4f *>(sc + 128 + kb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(S[kt][rt][i] - m_run[rt]);
-          lsum[rt] += pr;
+          const float pr = __builtin_amdgcn_exp2f(S[mt][4 * j + i] - m_use);
+          lsum += pr;
           const float pv = pr * vsc[i];
-          corr[rt] = fmaf(pv, vzc[i], corr[rt]);
-          pb[kt >> 1][rt][4 * (kt & 1) + i] = static_cast<_Float16>(pv);
+          corr = fmaf(pv, vzc[i], corr);
+          pb[2 * mt + (j >> 1)][4 * (j & 1) + i] = static_cast<_Float16>(pv);
         }
-    }
+      }
 
-    // ---- O^T += V^T P'^T
+    // ---- O^T += V^T P'^T (16-key steps st = 2*mt + j/2)
     const char *vbase = buf + T::V_OFF;
 #pragma unroll
     for (int dt = 0; dt < T::DT; ++dt) {
-      const int d = 16 * dt + r16;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + vt_offset<D>(d, 8 * s + g));
-        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + vt_offset<D>(d, 8 * s + 4 + g));
-        const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        const v8h vf = __builtin_bit_cast(v8h, w);
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          O[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[s][rt], O[dt][rt], 0, 0, 0);
+      for (int st = 0; st < 4; ++st) {
+        const int blk = 2 * dt * T::VBLK;
+        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + blk + v_off[2 * st]);
+        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + blk + v_off[2 * st + 1]);
+        const v8h vf = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[st], O[dt], 0, 0, 0);
       }
     }
 
     if (more) {
       wait_dma();
       __syncthreads();
-      convert_page<D>(a, p + 1, stage, smem + ((p + 1) & 1) * T::BUF, tid);
+      convert_page<D>(a, p + 1, stage, smem + (bi ^ 1) * T::BUF, tid);
     }
     __syncthreads();
   }
 
   // ---- finalize: O = (acc * 2^24|2^20 - corr) / l, written as [token][head][D]
+  float l = lsum, cz = corr;
+  {
+    auto a1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(a1[0]) + __uint_as_float(a1[1]);
+    auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(cz), __float_as_uint(cz), false, false);
+    cz = __uint_as_float(a2[0]) + __uint_as_float(a2[1]);
+  }
+  if (part) {
+    // Partial segment: O' = acc * 2^24|2^20 - corr (before the division), m, l.
+    const int lr = wave * 32 + r32;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = row0 + wave * 16 * RT + rt * 16 + r16;
-    const float l = xlane_sum16_32(lsum[rt]);
-    const float cz = xlane_sum16_32(corr[rt]);
-    if (row >= nrows) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int tok = row / 6, qh = h * 6 + row % 6;
-    const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * g;
+    for (int dt = 0; dt < T::DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < T::DT; ++dt) {
+      for (int j = 0; j < 4; ++j) {
+        v4f o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = O[dt][4 * j + i] * ((i & 1) ? 1048576.f : 16777216.f) - cz;
+        *reinterpret_cast<v4f *>(part + lr * D + 32 * dt + 8 * j + 4 * hh) = o;
+      }
+    if (hh == 0) {
+      part[128 * D + lr] = m_run;
+      part[128 * D + 128 + lr] = l;
+    }
+    return;
+  }
+  if (!row_valid) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int tok = row / 6, qh = h * 6 + row % 6;
+  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * hh;
+#pragma unroll
+  for (int dt = 0; dt < T::DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
       v4f o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (O[dt][rt][i] * ((i & 1) ? 1048576.f : 16777216.f) - cz) * inv;
-      store_out4(a.out, a.out_dtype, ob + 16 * dt, o);
+      for (int i = 0; i < 4; ++i) o[i] = (O[dt][4 * j + i] * ((i & 1) ? 1048576.f : 16777216.f) - cz) * inv;
+      store_out4(a.out, a.out_dtype, ob + 32 * dt + 8 * j, o);
     }
+}
+
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
+prefill_kernel(PrefillArgs a) {
+  using T = Tile<D>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * T::BUF + T::STAGE];
+  const int w = blockIdx.x;
+  const int v = a.xcd_perm ? (w % 8) * (a.grid / 8) + w / 8 : w;
+  const int s0 = range_start(a, v), s1 = range_start(a, v + 1);
+  if (s0 >= s1) return;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
+  int s = s0;
+  bool first = true;
+  while (s < s1) {
+    const int h = s / a.tper;
+    int rb, before;
+    locate_block(a, s - h * a.tper, lane, rb, before);
+    const int n = block_pages(a, rb);
+    const int p_lo = s - h * a.tper - before;
+    const int p_hi = min(n, p_lo + (s1 - s));
+    float *part = nullptr;
+    if (p_lo != 0 || p_hi != n)
+      part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * 128 * (D + 2);
+    run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+    s += p_hi - p_lo;
+    first = false;
   }
+}
+
+// Finishes the blocks split between work-groups: one work-group per block,
+// two threads per row, D/2 dims each.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  const int b = blockIdx.x;
+  const int h = b / a.nbh, rb = b % a.nbh;
+  const int lane = threadIdx.x % 64;
+  int start = 0;
+  {
+    // steps before block rb of head h
+    int base = 0;
+    for (int r0 = 0; r0 < rb; r0 += 64) {
+      const int r = r0 + lane;
+      int n = r < rb ? block_pages(a, r) : 0;
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
+      base += n;
+    }
+    start = h * a.tper + base;
+  }
+  const int n = block_pages(a, rb);
+  const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
+  if (va == vb) return;  // one work-group did the whole block
+  const int lr = threadIdx.x / 2, half = threadIdx.x % 2;
+  const int row = rb * 128 + lr;
+  if (row >= a.q_len * 6) return;
+  float M = -INFINITY;
+  for (int v = va; v <= vb; ++v) {
+    const int slot = range_start(a, v) >= start ? 0 : 1;
+    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * 128 * (D + 2);
+    M = fmaxf(M, pp[128 * D + lr]);
+  }
+  float l = 0.f;
+  v4f o[D / 8];
+#pragma unroll
+  for (int e = 0; e < D / 8; ++e) o[e] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int v = va; v <= vb; ++v) {
+    const int slot = range_start(a, v) >= start ? 0 : 1;
+    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * 128 * (D + 2);
+    const float m = pp[128 * D + lr];
+    if (m == -INFINITY) continue;
+    const float wgt = __builtin_amdgcn_exp2f(m - M);
+    l += wgt * pp[128 * D + 128 + lr];
+    const v4f *src = reinterpret_cast<const v4f *>(pp + lr * D + half * (D / 2));
+#pragma unroll
+    for (int e = 0; e < D / 8; ++e) o[e] += wgt * src[e];
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int tok = row / 6, qh = h * 6 + row % 6;
+  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + half * (D / 2);
+#pragma unroll
+  for (int e = 0; e < D / 8; ++e) store_out4(a.out, a.out_dtype, ob + 4 * e, o[e] * inv);
 }
 
 }  // namespace
 }  // namespace k8v4
+
+namespace k8v4 {
+namespace {
+
+struct PrefillPlan {
+  int nbh, tper, total, grid;
+};
+
+// Host mirror of the device schedule; false if the call is too large for it.
+bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, PrefillPlan &pl) {
+  const int64_t nbh = (q_len * kGqa + 127) / 128;
+  int64_t tper = 0;
+  for (int64_t rb = 0; rb < nbh; ++rb) {
+    const int64_t tok_hi = std::min<int64_t>(q_len - 1, (rb * 128 + 127) / 6);
+    tper += (seq_len - q_len + tok_hi + 1 + 63) / 64;
+  }
+  const int64_t total = tper * hkv;
+  if (nbh < 1 || total < 1 || total >= (int64_t(1) << 31) / 2) return false;
+  int64_t grid = std::min<int64_t>(2 * static_cast<int64_t>(device_cus()), total);
+  if (grid >= 8) grid -= grid % 8;
+  pl.nbh = static_cast<int>(nbh);
+  pl.tper = static_cast<int>(tper);
+  pl.total = static_cast<int>(total);
+  pl.grid = static_cast<int>(grid);
+  return true;
+}
+
+int64_t partial_bytes(int grid, int head_dim) {
+  return static_cast<int64_t>(grid) * 2 * 128 * (head_dim + 2) * 4;
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, int hkv, int head_dim) {
+  using namespace k8v4;
+  if (!supported_heads(hkv) || !supported_dim(head_dim) || q_len < 0 || q_len > seq_len) return -1;
+  if (q_len == 0) return 0;
+  PrefillPlan pl;
+  if (!plan_prefill(seq_len, q_len, hkv, pl)) return -1;
+  return partial_bytes(pl.grid, head_dim);
+}
 
 extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
                                   const float *k_scale, const uint8_t *v_cache, const float *v_scale,
@@ -452,7 +619,8 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
                                   int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
                                   int64_t vz_page_stride, const int32_t *block_row, int64_t table_width,
                                   int pages_per_block, int64_t seq_len, int64_t q_len, int hkv, int head_dim,
-                                  float scale, void *out, int out_dtype, int64_t out_tok_stride, void *stream) {
+                                  float scale, void *out, int out_dtype, int64_t out_tok_stride,
+                                  void *workspace, int64_t workspace_bytes, void *stream) {
   using namespace k8v4;
   clear_error();
   K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
@@ -510,24 +678,34 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   a.out_dtype = out_dtype;
   a.out_tok_stride = out_tok_stride;
 
-  const int rows_per_group = head_dim == 128 ? Tile<128>::ROWS : Tile<256>::ROWS;
-  const int64_t blocks = (q_len * kGqa + rows_per_group - 1) / rows_per_group;
-  K8V4_REQUIRE(blocks * hkv < (int64_t(1) << 31), "query chunk too long");
-  a.blocks = static_cast<int>(blocks);
-  int64_t grid;
-  const int per = 8 / hkv;  // row blocks of one head that share an XCD id group
-  if (blocks >= per) {
-    a.per_xcd = per;
-    const int64_t padded = (blocks + per - 1) / per * per;
-    grid = padded * hkv;
-  } else {
-    a.per_xcd = 0;
-    grid = blocks * hkv;
+  PrefillPlan pl;
+  K8V4_REQUIRE(plan_prefill(seq_len, q_len, hkv, pl), "prefill too large for one call (q_len %lld, seq_len %lld)",
+               static_cast<long long>(q_len), static_cast<long long>(seq_len));
+  const int64_t need = partial_bytes(pl.grid, head_dim);
+  K8V4_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "prefill workspace must be a 16-byte aligned device buffer");
+  if (workspace_bytes < need) {
+    set_error("prefill workspace holds %lld bytes, the call needs %lld", static_cast<long long>(workspace_bytes),
+              static_cast<long long>(need));
+    return K8V4_ERR_WORKSPACE;
   }
+  a.nbh = pl.nbh;
+  a.tper = pl.tper;
+  a.total = pl.total;
+  a.grid = pl.grid;
+  a.xcd_perm = pl.grid % 8 == 0 ? 1 : 0;
+  a.ws = static_cast<float *>(workspace);
   auto s = static_cast<hipStream_t>(stream);
   if (head_dim == 128)
-    prefill_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(a);
+    prefill_kernel<128><<<dim3(static_cast<unsigned>(pl.grid)), dim3(kThreads), 0, s>>>(a);
   else
-    prefill_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(a);
-  return launch_status("k8v4_prefill_paged");
+    prefill_kernel<256><<<dim3(static_cast<unsigned>(pl.grid)), dim3(kThreads), 0, s>>>(a);
+  const int rc = launch_status("k8v4_prefill_paged");
+  if (rc) return rc;
+  const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv));
+  if (head_dim == 128)
+    prefill_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
+  else
+    prefill_merge_kernel<256><<<mgrid, dim3(256), 0, s>>>(a);
+  return launch_status("k8v4_prefill_paged merge");
 }

@@ -70,9 +70,10 @@ _EXTRA_SYMBOLS.append(("k8v4_attn_batch_profiled", _EXTRA_SYMBOLS[0][1] + [_vp, 
 _EXTRA_SYMBOLS.append((
     "k8v4_prefill_paged",
     [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-     _vp, _i64, _i32, _i64, _i64, _i32, _i32, ctypes.c_float, _vp, _i32, _i64, _vp],
+     _vp, _i64, _i32, _i64, _i64, _i32, _i32, ctypes.c_float, _vp, _i32, _i64, _vp, _i64, _vp],
     _i32,
 ))
+_EXTRA_SYMBOLS.append(("k8v4_prefill_workspace_bytes", [_i64, _i64, _i32, _i32], _i64))
 
 
 def load_library():
@@ -333,17 +334,26 @@ class _Ops:
                          profiled=self._lib.k8v4_attn_batch_profiled)
 
     # -- chunked prefill ----------------------------------------------------
+    def prefill_workspace_bytes(self, seq_len: int, q_len: int, hkv: int, head_dim: int) -> int:
+        """Scratch bytes :meth:`prefill_paged` needs for this shape."""
+        n = int(self._lib.k8v4_prefill_workspace_bytes(int(seq_len), int(q_len), int(hkv), int(head_dim)))
+        _require(n >= 0, "bad shape for the prefill workspace")
+        return n
+
     def prefill_paged(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len: int,
-                      pages_per_block: int, scale: float, out):
+                      pages_per_block: int, scale: float, out, workspace=None):
         """Bottom-right causal attention of ``q [q_len, HQ, D]`` over one sequence's pages into ``out``."""
         call = self.bind_prefill_paged(q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len,
-                                       pages_per_block, scale, out)
+                                       pages_per_block, scale, out, workspace)
         if call is not None:
             call()
 
     def bind_prefill_paged(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len: int,
-                           pages_per_block: int, scale: float, out):
-        """Validate one prefill; returns a :class:`BoundCall` (None when ``q_len`` is 0)."""
+                           pages_per_block: int, scale: float, out, workspace=None):
+        """Validate one prefill; returns a :class:`BoundCall` (None when ``q_len`` is 0).
+
+        ``workspace`` is a device buffer of at least :meth:`prefill_workspace_bytes`
+        bytes; None allocates one (the prefill path is not graph-captured)."""
         _require(q.dim() == 3, "query [T,HQ,D]")
         head_dim = int(q.shape[2])
         _require(head_dim in (128, 256), "query [T,HQ,D] with D in (128, 256)")
@@ -368,12 +378,19 @@ class _Ops:
         _require(int(pages_per_block) >= 1, "pages_per_block")
         tensors = (q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, out)
         dev = _on_gpu(*tensors)
+        need = self.prefill_workspace_bytes(seq_len, q_len, hkv, head_dim)
+        if workspace is None:
+            workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=dev)
+        _require(workspace.is_contiguous() and workspace.device == dev, "prefill workspace must be a contiguous "
+                 "buffer on the query's device")
+        tensors = tensors + (workspace,)
         args = [
             _ptr(q), _DTYPE_CODE[q.dtype], int(q.stride(0)) if q_len > 1 else GQA * hkv * head_dim,
             *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
             _ptr(block_row), int(block_row.shape[0]), int(pages_per_block), seq_len, q_len, hkv, head_dim,
             float(scale), _ptr(out), _DTYPE_CODE[out.dtype],
             int(out.stride(0)) if q_len > 1 else GQA * hkv * head_dim,
+            _ptr(workspace), int(workspace.numel()) * workspace.element_size(),
         ]
         return BoundCall(self._lib, self._lib.k8v4_prefill_paged, args, dev, tensors)
 

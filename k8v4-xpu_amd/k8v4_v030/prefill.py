@@ -28,6 +28,7 @@ def hip_prefill(
     pages_per_block: int,
     scale: float,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Bottom-right causal attention of the last ``q_len`` tokens of a sequence."""
     q_len = int(query.shape[0])
@@ -47,7 +48,7 @@ def hip_prefill(
     if row.dtype != torch.int32 or not row.is_contiguous():
         row = row.to(torch.int32).contiguous()
     ops().prefill_paged(query, views["k"], views["k_scale"], views["v"], views["v_scale"], views["v_zero"],
-                        row, seq_len, pages_per_block, scale, out)
+                        row, seq_len, pages_per_block, scale, out, workspace)
     return out
 
 

@@ -35,7 +35,8 @@ def lib():
 def test_header_declares_the_entry_points():
     names = set(_declared())
     assert {"k8v4_abi_version", "k8v4_last_error", "k8v4_kv_store_paged", "k8v4_attn_batch",
-            "k8v4_attn_batch_profiled", "k8v4_attn_workspace_bytes"} <= names
+            "k8v4_attn_batch_profiled", "k8v4_attn_workspace_bytes", "k8v4_prefill_paged",
+            "k8v4_prefill_workspace_bytes"} <= names
 
 
 def test_every_declared_symbol_is_exported_and_bound(lib):

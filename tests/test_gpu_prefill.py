@@ -141,3 +141,20 @@ def test_prefill_chunk_4224_over_131072_sampled_rows(gpu_ops):
     want = _oracle(cache, q, table[0], seq_len, rows=rows)
     err = assert_close(got[rows], want, what="4224x131072")
     print("  sampled rows max abs err %.2e" % err, flush=True)
+
+
+@pytest.mark.parametrize("q_len,seq_len", [(3, 5000), (1, 64), (40, 40), (500, 9000)])
+def test_prefill_blocks_split_across_many_work_groups(gpu_ops, q_len, seq_len):
+    """Short chunks over long contexts: the balanced schedule cuts one row block into
+    many pieces (down to single pages, some with no visible key for early rows)
+    that the merge kernel combines."""
+    lay = PageLayout(4, 128)
+    gen = torch.Generator().manual_seed(q_len + seq_len)
+    pool = (seq_len + PAGE - 1) // PAGE + 3
+    table = random_tables(gen, [seq_len], pool)
+    cache = Cache(pool, lay)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len)
+    q = seeded_normal(gen, (q_len, 24, 128))
+    got = _run(cache, q, table[0], seq_len).float().cpu().numpy()
+    assert_close(got, _oracle(cache, q, table[0], seq_len), what="split blocks")
+    assert gpu_ops.prefill_workspace_bytes(seq_len, q_len, 4, 128) > 0
