@@ -42,7 +42,6 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr float kThreshold = 8.0f;
-constexpr int kThreads = 256;  // four waves
 constexpr uint32_t kEvenNib = 0x000F000Fu;
 constexpr uint32_t kOddNib = 0x00F000F0u;
 
@@ -63,12 +62,13 @@ struct PrefillArgs {
   int q_len;
   int hkv;
   float c;       // softmax scale * log2(e)
-  int nbh;       // 128-row blocks per KV head
+  int rows;      // query rows per block (32 per wave of a work-group)
+  int nbh;       // row blocks per KV head
   int tper;      // page steps of one head: sum over its blocks of the pages each reads
   int total;     // page steps of the call (hkv * tper)
   int grid;      // persistent work-groups; work-group v takes steps [v*total/grid, (v+1)*total/grid)
   int xcd_perm;  // map ids so the work-groups of one XCD take adjacent work (grid % 8 == 0)
-  float *ws;     // partial states: [grid][2][128 rows][D + 2] floats
+  float *ws;     // partial states: [grid][2][rows][D + 2] floats
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -76,8 +76,12 @@ struct PrefillArgs {
 
 template <int D>
 struct Tile {
-  static constexpr int WPE = D == 128 ? 2 : 1;       // waves per SIMD (LDS: one group per CU at D=256)
-  static constexpr int ROWS = 4 * 32;                // query rows per work-group (one 32-row tile per wave)
+  // D=128: eight waves (two per SIMD) share each converted page; D=256: four
+  // waves (one per SIMD, the register file holds the wider accumulators).
+  static constexpr int NW = D == 128 ? 8 : 4;        // waves per work-group, one work-group per CU
+  static constexpr int WPE = NW / 4;                 // waves per SIMD
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int ROWS = 32 * NW;               // query rows per block (one 32-row tile per wave)
   static constexpr int DS = D / 16;                  // k-steps of the QK MFMA (16 dims each)
   static constexpr int DT = D / 32;                  // 32-dim output tiles
   // MFMA tile of one page (one ring buffer).  Row paddings, not XOR
@@ -93,9 +97,10 @@ struct Tile {
   // planes go straight into the S area of the ring buffer they belong to).
   static constexpr int SV_OFF = 64 * D;
   static constexpr int STAGE = SV_OFF + 32 * D;
-  static constexpr int KCH = 64 * D / 16 / kThreads;   // 16-byte K pieces per thread
-  static constexpr int VCH = 32 * D / 16 / kThreads;   // 16-byte V pieces per thread
-  static constexpr int VIT = 32 * (D / 16) / kThreads;  // (key pair, 8-byte group) items per thread
+  static constexpr int KDMA = D / 16;                 // 1 KB K pieces per page (one DMA each)
+  static constexpr int VDMA = D / 32;                 // 1 KB V pieces per page
+  static constexpr int KCHUNKS = 4 * D;               // 16-byte K code chunks per page
+  static constexpr int VITEMS = 2 * D;                // (key pair, 8-byte group) V items per page
 };
 
 template <int D>
@@ -124,9 +129,9 @@ __device__ __forceinline__ void dma4(const void *src, lds_t *dst) {
   __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 4, 0, 0);
 }
 
-// Wave w, lane L: 16-byte K pieces 64 * (4 j + w) + L (row-major codes), V
-// pieces likewise, and scale plane w (waves 0-2) for key L, the latter into the
-// S area of the ring buffer the page will be converted into.
+// DMA idx (taken by wave idx % NW), lane L: 16-byte K piece 64 * idx + L
+// (row-major codes), V pieces likewise, and scale plane w (waves 0-2) for key
+// L, the latter into the S area of the ring buffer the page is converted into.
 template <int D>
 __device__ __forceinline__ void stage_page(const PrefillArgs &a, int p, int h, int wave, int lane, lds_t *stage,
                                            lds_t *scales) {
@@ -135,16 +140,22 @@ __device__ __forceinline__ void stage_page(const PrefillArgs &a, int p, int h, i
   const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + h * D;
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps + h * (D / 2);
 #pragma unroll
-  for (int j = 0; j < T::KCH; ++j) {
-    const int c = 64 * (4 * j + wave) + lane;
-    const int key = c / (D / 16), part = c % (D / 16);
-    dma16(kb + static_cast<int64_t>(key) * a.hkv * D + part * 16, stage + 1024 * (4 * j + wave));
+  for (int j = 0; j < (T::KDMA + T::NW - 1) / T::NW; ++j) {
+    const int idx = T::NW * j + wave;
+    if (idx < T::KDMA) {
+      const int c = 64 * idx + lane;
+      const int key = c / (D / 16), part = c % (D / 16);
+      dma16(kb + static_cast<int64_t>(key) * a.hkv * D + part * 16, stage + 1024 * idx);
+    }
   }
 #pragma unroll
-  for (int j = 0; j < T::VCH; ++j) {
-    const int c = 64 * (4 * j + wave) + lane;
-    const int key = c / (D / 32), part = c % (D / 32);
-    dma16(vb + static_cast<int64_t>(key) * a.hkv * (D / 2) + part * 16, stage + T::SV_OFF + 1024 * (4 * j + wave));
+  for (int j = 0; j < (T::VDMA + T::NW - 1) / T::NW; ++j) {
+    const int idx = T::NW * j + wave;
+    if (idx < T::VDMA) {
+      const int c = 64 * idx + lane;
+      const int key = c / (D / 32), part = c % (D / 32);
+      dma16(vb + static_cast<int64_t>(key) * a.hkv * (D / 2) + part * 16, stage + T::SV_OFF + 1024 * idx);
+    }
   }
   if (wave < 3) {
     const float *plane = wave == 0 ? a.k_scale : wave == 1 ? a.v_scale : a.v_zero;
@@ -170,8 +181,9 @@ template <int D>
 __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const char *stage, char *buf, int tid) {
   using T = Tile<D>;
 #pragma unroll
-  for (int j = 0; j < T::KCH; ++j) {
-    const int c = tid + kThreads * j;
+  for (int j = 0; j < (T::KCHUNKS + T::THREADS - 1) / T::THREADS; ++j) {
+    const int c = tid + T::THREADS * j;
+    if (c >= T::KCHUNKS) break;
     const int key = c / (D / 16), part = c % (D / 16);
     const uint4 w = *reinterpret_cast<const uint4 *>(stage + 16 * c);
     v2h h[8];
@@ -188,8 +200,9 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
     *reinterpret_cast<uint4 *>(row + 32 * part + 16) = c1;
   }
 #pragma unroll
-  for (int j = 0; j < T::VIT; ++j) {
-    const int it = tid + kThreads * j;
+  for (int j = 0; j < (T::VITEMS + T::THREADS - 1) / T::THREADS; ++j) {
+    const int it = tid + T::THREADS * j;
+    if (it >= T::VITEMS) break;
     const int pair = it / (D / 16), grp = it % (D / 16);
     const uint2 v0 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair) * (D / 2) + 8 * grp);
     const uint2 v1 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair + 1) * (D / 2) + 8 * grp);
@@ -240,7 +253,7 @@ __device__ __forceinline__ void store_out4(void *out, int dtype, int64_t idx, v4
 // goes to slot 0 if v's range starts inside the block, else to slot 1.
 
 __device__ __forceinline__ int block_pages(const PrefillArgs &a, int rb) {
-  const int tok_hi = min(a.q_len - 1, (rb * 128 + 127) / 6);
+  const int tok_hi = min(a.q_len - 1, (rb * a.rows + a.rows - 1) / 6);
   return (a.seq_len - a.q_len + tok_hi + 1 + 63) / 64;
 }
 
@@ -463,8 +476,8 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
         *reinterpret_cast<v4f *>(part + lr * D + 32 * dt + 8 * j + 4 * hh) = o;
       }
     if (hh == 0) {
-      part[128 * D + lr] = m_run;
-      part[128 * D + 128 + lr] = l;
+      part[T::ROWS * D + lr] = m_run;
+      part[T::ROWS * D + T::ROWS + lr] = l;
     }
     return;
   }
@@ -484,7 +497,7 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
 }
 
 template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+__global__ __attribute__((amdgpu_flat_work_group_size(Tile<D>::THREADS, Tile<D>::THREADS),
                           amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
 prefill_kernel(PrefillArgs a) {
   using T = Tile<D>;
@@ -507,7 +520,7 @@ prefill_kernel(PrefillArgs a) {
     const int p_hi = min(n, p_lo + (s1 - s));
     float *part = nullptr;
     if (p_lo != 0 || p_hi != n)
-      part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * 128 * (D + 2);
+      part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * T::ROWS * (D + 2);
     run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     s += p_hi - p_lo;
     first = false;
@@ -517,7 +530,8 @@ prefill_kernel(PrefillArgs a) {
 // Finishes the blocks split between work-groups: one work-group per block,
 // two threads per row, D/2 dims each.
 template <int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(2 * Tile<D>::ROWS) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int R = Tile<D>::ROWS;
   const int b = blockIdx.x;
   const int h = b / a.nbh, rb = b % a.nbh;
   const int lane = threadIdx.x % 64;
@@ -538,13 +552,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
   if (va == vb) return;  // one work-group did the whole block
   const int lr = threadIdx.x / 2, half = threadIdx.x % 2;
-  const int row = rb * 128 + lr;
+  const int row = rb * R + lr;
   if (row >= a.q_len * 6) return;
   float M = -INFINITY;
   for (int v = va; v <= vb; ++v) {
     const int slot = range_start(a, v) >= start ? 0 : 1;
-    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * 128 * (D + 2);
-    M = fmaxf(M, pp[128 * D + lr]);
+    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * R * (D + 2);
+    M = fmaxf(M, pp[R * D + lr]);
   }
   float l = 0.f;
   v4f o[D / 8];
@@ -552,11 +566,11 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   for (int e = 0; e < D / 8; ++e) o[e] = (v4f){0.f, 0.f, 0.f, 0.f};
   for (int v = va; v <= vb; ++v) {
     const int slot = range_start(a, v) >= start ? 0 : 1;
-    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * 128 * (D + 2);
-    const float m = pp[128 * D + lr];
+    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * R * (D + 2);
+    const float m = pp[R * D + lr];
     if (m == -INFINITY) continue;
     const float wgt = __builtin_amdgcn_exp2f(m - M);
-    l += wgt * pp[128 * D + 128 + lr];
+    l += wgt * pp[R * D + R + lr];
     const v4f *src = reinterpret_cast<const v4f *>(pp + lr * D + half * (D / 2));
 #pragma unroll
     for (int e = 0; e < D / 8; ++e) o[e] += wgt * src[e];
@@ -579,16 +593,19 @@ struct PrefillPlan {
 };
 
 // Host mirror of the device schedule; false if the call is too large for it.
-bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, PrefillPlan &pl) {
-  const int64_t nbh = (q_len * kGqa + 127) / 128;
+int rows_per_block(int head_dim) { return head_dim == 128 ? Tile<128>::ROWS : Tile<256>::ROWS; }
+
+bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, int head_dim, PrefillPlan &pl) {
+  const int64_t R = rows_per_block(head_dim);
+  const int64_t nbh = (q_len * kGqa + R - 1) / R;
   int64_t tper = 0;
   for (int64_t rb = 0; rb < nbh; ++rb) {
-    const int64_t tok_hi = std::min<int64_t>(q_len - 1, (rb * 128 + 127) / 6);
+    const int64_t tok_hi = std::min<int64_t>(q_len - 1, (rb * R + R - 1) / 6);
     tper += (seq_len - q_len + tok_hi + 1 + 63) / 64;
   }
   const int64_t total = tper * hkv;
   if (nbh < 1 || total < 1 || total >= (int64_t(1) << 31) / 2) return false;
-  int64_t grid = std::min<int64_t>(2 * static_cast<int64_t>(device_cus()), total);
+  int64_t grid = std::min<int64_t>(static_cast<int64_t>(device_cus()), total);  // one work-group per CU
   if (grid >= 8) grid -= grid % 8;
   pl.nbh = static_cast<int>(nbh);
   pl.tper = static_cast<int>(tper);
@@ -598,7 +615,7 @@ bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, PrefillPlan &pl) {
 }
 
 int64_t partial_bytes(int grid, int head_dim) {
-  return static_cast<int64_t>(grid) * 2 * 128 * (head_dim + 2) * 4;
+  return static_cast<int64_t>(grid) * 2 * rows_per_block(head_dim) * (head_dim + 2) * 4;
 }
 
 }  // namespace
@@ -609,7 +626,7 @@ extern "C" int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, 
   if (!supported_heads(hkv) || !supported_dim(head_dim) || q_len < 0 || q_len > seq_len) return -1;
   if (q_len == 0) return 0;
   PrefillPlan pl;
-  if (!plan_prefill(seq_len, q_len, hkv, pl)) return -1;
+  if (!plan_prefill(seq_len, q_len, hkv, head_dim, pl)) return -1;
   return partial_bytes(pl.grid, head_dim);
 }
 
@@ -679,7 +696,7 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   a.out_tok_stride = out_tok_stride;
 
   PrefillPlan pl;
-  K8V4_REQUIRE(plan_prefill(seq_len, q_len, hkv, pl), "prefill too large for one call (q_len %lld, seq_len %lld)",
+  K8V4_REQUIRE(plan_prefill(seq_len, q_len, hkv, head_dim, pl), "prefill too large for one call (q_len %lld, seq_len %lld)",
                static_cast<long long>(q_len), static_cast<long long>(seq_len));
   const int64_t need = partial_bytes(pl.grid, head_dim);
   K8V4_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
@@ -689,6 +706,7 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
               static_cast<long long>(need));
     return K8V4_ERR_WORKSPACE;
   }
+  a.rows = rows_per_block(head_dim);
   a.nbh = pl.nbh;
   a.tper = pl.tper;
   a.total = pl.total;
@@ -697,15 +715,15 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   a.ws = static_cast<float *>(workspace);
   auto s = static_cast<hipStream_t>(stream);
   if (head_dim == 128)
-    prefill_kernel<128><<<dim3(static_cast<unsigned>(pl.grid)), dim3(kThreads), 0, s>>>(a);
+    prefill_kernel<128><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<128>::THREADS), 0, s>>>(a);
   else
-    prefill_kernel<256><<<dim3(static_cast<unsigned>(pl.grid)), dim3(kThreads), 0, s>>>(a);
+    prefill_kernel<256><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<256>::THREADS), 0, s>>>(a);
   const int rc = launch_status("k8v4_prefill_paged");
   if (rc) return rc;
   const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv));
   if (head_dim == 128)
-    prefill_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
+    prefill_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS), 0, s>>>(a);
   else
-    prefill_merge_kernel<256><<<mgrid, dim3(256), 0, s>>>(a);
+    prefill_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS), 0, s>>>(a);
   return launch_status("k8v4_prefill_paged merge");
 }
