@@ -166,6 +166,53 @@ __device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want
   return r;
 }
 
+// The split kernel's view of the plan in one pass over the lengths when the
+// batch fits one wave (the common case): pages per split P, the split range
+// of work-group wg, and that sequence's page count and length.
+struct SplitPlan {
+  SplitRange r;
+  int P;
+  int npages;
+  int L0;
+};
+
+__device__ SplitPlan plan_split(const DecodeArgs &a, int lane, int wg) {
+  SplitPlan sp;
+  if (a.batch > kWave) {
+    sp.P = plan_pages_per_split(a, lane);
+    sp.r = plan_locate(a, sp.P, lane, -1, wg);
+    sp.npages = sp.r.b >= 0 ? seq_pages(a, sp.r.b) : 0;
+    sp.L0 = sp.r.b >= 0 ? seq_len0(a, sp.r.b) : 0;
+    return sp;
+  }
+  const int L = lane < a.batch ? seq_len0(a, lane) : 0;
+  int n = 0;
+  if (L > 0) {
+    const int64_t cap = static_cast<int64_t>(a.table_width) * a.ppb;
+    const int64_t np = (static_cast<int64_t>(L) + kPage - 1) / kPage;
+    n = static_cast<int>(np < cap ? np : cap);
+  }
+  const int total = wave_sum(n), maxn = wave_max(n);
+  int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
+  P = __builtin_amdgcn_readfirstlane(max(max(P, a.min_pages), 1));
+  const int s = (n + P - 1) / P;
+  const int excl = wave_inclusive_scan(s, lane) - s;
+  const uint64_t mask = __ballot(s > 0 && wg >= excl && wg < excl + s);
+  sp.P = P;
+  sp.r = SplitRange{-1, 0, 0};
+  sp.npages = 0;
+  sp.L0 = 0;
+  if (mask) {
+    const int src = __builtin_ctzll(mask);
+    sp.r.b = __builtin_amdgcn_readfirstlane(src);
+    sp.r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, src, kWave));
+    sp.r.count = __builtin_amdgcn_readfirstlane(__shfl(s, src, kWave));
+    sp.npages = __builtin_amdgcn_readfirstlane(__shfl(n, src, kWave));
+    sp.L0 = __builtin_amdgcn_readfirstlane(__shfl(L, src, kWave));
+  }
+  return sp;
+}
+
 // Block-table reads go through the constant address space: the table is
 // read-only for the kernel's lifetime, so a uniform lookup becomes a scalar
 // load and never waits on the vector-memory counter the LDS DMA uses.
@@ -274,7 +321,7 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int h, int n, int g, int lan
 // loads (from page 0) so every chunk costs the same vmcnt.  K and V move in
 // 16-byte-per-lane DMAs from a wave-uniform base plus a 32-bit lane offset;
 // the scale planes of this head are gathered with two 4-byte DMAs (lanes
-// 0-31: k_scale then v_zero, lanes 32-63: v_scale then v_zero again).
+// 0-31: k_scale then v_scale, lanes 32-63: v_scale then v_zero).
 template <int D, int HKV>
 __device__ __forceinline__ int issue_k(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
                                        lds_t *kslot) {
@@ -308,8 +355,11 @@ __device__ __forceinline__ void issue_v(const DecodeArgs &a, const int32_t *bt_r
   const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0;
   const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0;
   const char *vzp = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + plane0;
-  dma4(lane < 32 ? ksp : vsp, vslot + S::S_OFF);        // ks[32] | vs[32]
-  if (lane < 32) dma4(vzp, vslot + S::S_OFF + 256);     // vz[32]
+  // Two full-wave 4-byte DMAs, no divergent branch: ks[32] | vs[32] at
+  // S_OFF, then vs[32] | vz[32] at S_OFF + 128 (the v_scale cells are written
+  // twice with the same values).
+  dma4(lane < 32 ? ksp : vsp, vslot + S::S_OFF);
+  dma4(lane < 32 ? vsp : vzp, vslot + S::S_OFF + 128);
 }
 
 // Wait until at most `after` chunks' DMAs are still in flight.
@@ -567,9 +617,10 @@ template <int D, int NT, int HKV, int NWH>
 struct SplitConfig {
   // Two waves per head keep the int8 Q operands in LDS (shared by the pair);
   // one wave per head keeps Q in registers.  Each wave owns a K ring of RK
-  // slots and a V ring of RV slots, as deep as the LDS allows: a K slot is
-  // refilled as soon as its QK^T product is issued, so while a wave computes
-  // one chunk up to RK - 1 K slots and RV - 1 V slots are in flight.
+  // slots and a V ring of RV slots, the K ring as deep as the LDS allows;
+  // with two waves per SIMD a K slot is refilled as soon as its QK^T product
+  // is issued, so while a wave computes one chunk up to RK - 1 K slots and
+  // RV - 1 V slots are in flight.
   static constexpr bool QLDS = NWH > 1;
   static constexpr int WAVES = HKV * NWH;
   static constexpr int Q_FRAG_BYTES = NT * (D / 64) * kWave * 16;         // int8 B-operand fragments
@@ -577,6 +628,10 @@ struct SplitConfig {
   static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
   // 4 / HKV work-groups share a CU (the grid is about that many per CU).
   static constexpr int LDS_MAX = 163840 * HKV / 4;
+  // One wave per SIMD (NWH == 1) has no partner wave to cover the table
+  // lookup of a mid-chunk refill: it refills its K slot after P.V, next to
+  // the V slot.
+  static constexpr bool K_EARLY = NWH > 1;
   static constexpr int RV = 2;
   static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
   static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
@@ -609,12 +664,13 @@ void decode_split_kernel(DecodeArgs a) {
   const int w = wave / HKV;   // position among the NWH waves of this head
   const int n = lane & 15, g = lane >> 4;
 
-  const int P = plan_pages_per_split(a, lane);
-  const SplitRange sr = plan_locate(a, P, lane, -1, static_cast<int>(blockIdx.x));
+  const SplitPlan plan = plan_split(a, lane, static_cast<int>(blockIdx.x));
+  const SplitRange sr = plan.r;
   if (sr.b < 0) return;  // idle work-group (uniform over the work-group)
+  const int P = plan.P;
   const int b = sr.b;
-  const int npages = seq_pages(a, b);
-  const int L0 = seq_len0(a, b);
+  const int npages = plan.npages;
+  const int L0 = plan.L0;
   const int p0 = (static_cast<int>(blockIdx.x) - sr.first) * P;
   const int p1 = min(npages, p0 + P);
   const int x0 = 2 * p0;
@@ -622,36 +678,34 @@ void decode_split_kernel(DecodeArgs a) {
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
 
-  // This wave's chunks: x0 + w + k*NWH for k < cnt.
-  const int my0 = x0 + w;
-  const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
-  lds_t *kring = lds + wave * CFG::WAVE_BYTES;
-  lds_t *vring = kring + RK * S::K_BYTES;
-  const LaneOffsets lo = lane_offsets<D, HKV>(h, n, g, lane);
-  // DMA bookkeeping (wave-uniform): `issued` counts this wave's DMA
-  // instructions; mk[s] / mv[s] is the count right after the K / V group of
-  // ring slot s was issued, so a chunk is resident once at most
-  // issued - max(mk, mv) loads remain outstanding (loads complete in order).
-  int issued = 0;
-  int mk[4] = {0, 0, 0, 0}, mv[2] = {0, 0};
-  uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
+  // Raw query words of this wave's Q tiles, loaded before the ring's first
+  // DMAs so they do not wait behind them (vector loads complete in order).
+  uint4 qraw[NT][KS][2];
 #pragma unroll
-  for (int s = 0; s < RK; ++s) {
-    if (s < cnt) {
-      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + s * NWH, lo, kring + s * S::K_BYTES)) << s;
-      issued += S::NK;
-      mk[s] = issued;
-      if (s < RV) {
-        issue_v<D, HKV>(a, bt_row, my0 + s * NWH, lo, lane, vring + s * S::V_BYTES);
-        issued += S::NVS;
-        mv[s] = issued;
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (CFG::QLDS) {
+      if (nt % NWH != w) continue;  // the partner wave quantizes this tile
+    }
+    const int r = 16 * nt + n;
+    if (r < rows) {
+      const int j = r / kGqa;
+      const int qh = h * kGqa + (r - j * kGqa);
+      const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
+                            static_cast<int64_t>(qh) * D;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qraw[nt][ks][0] = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g);
+        qraw[nt][ks][1] = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g + 8);
       }
     }
   }
 
   WaveState<D, NT, CFG::QLDS> st;
   lds_t *qlds = lds + CFG::Q_OFF + h * CFG::Q_BYTES_PER_HEAD;
-  // Causal ends: row r (token j = r / 6) sees keys t < lim(r).
+  // Causal ends, also read before the first DMAs: row r (token j = r / 6)
+  // sees keys t < lim(r).
   int min_end = L0;
   for (int j = 0; j < a.q_len; ++j) {
     const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
@@ -669,6 +723,39 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
 
+  // This wave's chunks: x0 + w + k*NWH for k < cnt.
+  const int my0 = x0 + w;
+  const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
+  lds_t *kring = lds + wave * CFG::WAVE_BYTES;
+  lds_t *vring = kring + RK * S::K_BYTES;
+  const LaneOffsets lo = lane_offsets<D, HKV>(h, n, g, lane);
+  // DMA bookkeeping (wave-uniform): `issued` counts this wave's DMA
+  // instructions; mk[s] / mv[s] is the count right after the K / V group of
+  // ring slot s was issued, so a chunk is resident once at most
+  // issued - max(mk, mv) loads remain outstanding (loads complete in order).
+  // The compiler makes the first use of the Q words wait for every vector
+  // load issued before it, ring DMAs included, so only the first chunk's K
+  // and V groups go out before the quantization; the rest of the ring is
+  // filled right after it.
+  int issued = 0;
+  int mk[4] = {0, 0, 0, 0}, mv[4] = {0, 0, 0, 0};
+  uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
+  auto fill_slot = [&](int s) {
+    if (s >= cnt) return;
+    const int xs = my0 + s * NWH;
+    if (s < RK) {
+      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, xs, lo, kring + s * S::K_BYTES)) << s;
+      issued += S::NK;
+      mk[s] = issued;
+    }
+    if (s < RV) {
+      issue_v<D, HKV>(a, bt_row, xs, lo, lane, vring + s * S::V_BYTES);
+      issued += S::NVS;
+      mv[s] = issued;
+    }
+  };
+  fill_slot(0);
+
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
   // both waves of the head quantize (they need crow) and wave 0 stores.
@@ -679,29 +766,16 @@ void decode_split_kernel(DecodeArgs a) {
       if constexpr (CFG::QLDS) {
         if (nt % NWH != w) continue;  // the partner wave quantizes this tile
       }
-      const int r = 16 * nt + n;
       float x[KS][16];
-      if (r < rows) {
-        const int j = r / kGqa;
-        const int qh = h * kGqa + (r - j * kGqa);
-        const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
-                              static_cast<int64_t>(qh) * D;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const uint4 w0 = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g);
-          const uint4 w1 = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g + 8);
-          const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 w0 = qraw[nt][ks][0], w1 = qraw[nt][ks][1];
+        const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            x[ks][2 * e] = half_bits_to_float(static_cast<uint16_t>(words[e] & 0xFFFFu), a.q_bf16);
-            x[ks][2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(words[e] >> 16), a.q_bf16);
-          }
+        for (int e = 0; e < 8; ++e) {
+          x[ks][2 * e] = half_bits_to_float(static_cast<uint16_t>(words[e] & 0xFFFFu), a.q_bf16);
+          x[ks][2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(words[e] >> 16), a.q_bf16);
         }
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) x[ks][e] = 0.f;
       }
       float amax = 0.f;
 #pragma unroll
@@ -711,15 +785,29 @@ void decode_split_kernel(DecodeArgs a) {
       amax = xlane_max16_32(amax);
       const double scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
       const double inv = amax == 0.f ? 0.0 : 1.0 / scale;
+      const float inv32 = static_cast<float>(inv);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         uint32_t wq[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const double y = static_cast<double>(x[ks][e]) * inv;
-          double qv = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
-          qv = fmin(fmax(qv, -127.0), 127.0);
-          wq[e >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(qv)) & 0xFFu) << (8 * (e & 3));
+          // fp32 product (within 127 * 2^-23 of the float64 one); only a
+          // value whose fraction lies within 2^-12 of one half is redone in
+          // float64 as the reference computes it.
+          const float y32 = x[ks][e] * inv32;
+          const float ay = fabsf(y32);
+          const float fl = floorf(ay);
+          const float fr = ay - fl;
+          int32_t qi;
+          if (fabsf(fr - 0.5f) < 2.44140625e-4f) {
+            const double y = static_cast<double>(x[ks][e]) * inv;
+            double qv = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
+            qi = static_cast<int32_t>(fmin(fmax(qv, -127.0), 127.0));
+          } else {
+            const int32_t qa = static_cast<int32_t>(fminf(fl + (fr > 0.5f ? 1.f : 0.f), 127.f));
+            qi = y32 < 0.f ? -qa : qa;
+          }
+          wq[e >> 2] |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * (e & 3));
         }
         const v4i frag = (v4i){static_cast<int>(wq[0]), static_cast<int>(wq[1]), static_cast<int>(wq[2]),
                                static_cast<int>(wq[3])};
@@ -739,6 +827,9 @@ void decode_split_kernel(DecodeArgs a) {
       }
     }
   }
+
+#pragma unroll
+  for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
 
   if constexpr (CFG::QLDS) {
     __syncthreads();  // Q fragments and row factors visible to both waves of the head
@@ -765,13 +856,15 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 1; s < RK; ++s)
       if (sk == s) mks = mk[s];
-    if (sv == 1) mvs = mv[1];
+#pragma unroll
+    for (int s = 1; s < RV; ++s)
+      if (sv == s) mvs = mv[s];
     wait_vm(issued - max(mks, mvs));
     const bool valid = (valid_mask >> sk) & 1u;
     const int tbase = 32 * (my0 + k * NWH);
     v4i sc[2][NT];
     if (valid) chunk_qk<D, NT, CFG::QLDS>(st, kslot, qlds, lane, g, sc);
-    if (k + RK < cnt) {
+    if (CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + (k + RK) * NWH, lo, kslot));
@@ -782,11 +875,23 @@ void decode_split_kernel(DecodeArgs a) {
         if (sk == s) mk[s] = issued;
     }
     if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+    if (!CFG::K_EARLY && k + RK < cnt) {
+      // The K reads of this slot have completed (their values fed the MFMAs).
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + (k + RK) * NWH, lo, kslot));
+      valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
+      issued += S::NK;
+#pragma unroll
+      for (int s = 0; s < RK; ++s)
+        if (sk == s) mk[s] = issued;
+    }
     if (k + RV < cnt) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue_v<D, HKV>(a, bt_row, my0 + (k + RV) * NWH, lo, lane, vslot);
       issued += S::NVS;
-      if (sv == 0) mv[0] = issued; else mv[1] = issued;
+#pragma unroll
+      for (int s = 0; s < RV; ++s)
+        if (sv == s) mv[s] = issued;
     }
   }
 
