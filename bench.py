@@ -52,6 +52,8 @@ def parse_args(argv=None):
     ap.add_argument("--splits", type=int, default=0, help="split-K work-groups (0 = library default)")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", default=None,
+                    help="run only the config rows whose name contains this text (no headline; for profiling)")
     return ap.parse_args(argv)
 
 
@@ -363,10 +365,15 @@ def cpu_baseline(torch, work, min_seconds=10.0, max_reps=5):
 
 
 # --------------------------------------------------------------------- configs
-def config_rows(torch, hip, ops, steps, warmup):
+def config_rows(torch, hip, ops, steps, warmup, only=None):
     rows = {}
 
+    def want(name):
+        return only is None or only in name
+
     def decode_row(name, lengths, q_len, copies, seed, hkv=4, head_dim=128, **kw):
+        if not want(name):
+            return
         w = DecodeWorkload(ops, torch, lengths=lengths, q_len=q_len, hkv=hkv, head_dim=head_dim,
                            copies=copies, seed=seed, **kw)
         warm_clocks(torch, w, 1.0)
@@ -385,37 +392,39 @@ def config_rows(torch, hip, ops, steps, warmup):
         progress("%s: %.2f us/layer" % (name, us))
 
     decode_row("1_decode_ctx2048_q1", [2048], 1, copies=128, seed=1001, pool_pages_per_copy=64)
-    w = StoreWorkload(ops, torch, copies=8, seed=1002)
-    warm_clocks(torch, w, 1.0)
-    us = kernel_us(torch, hip, w, 3, steps, warmup)
-    rows["2_store_4x4224_tokens"] = {
-        "us_per_layer": round(us, 2),
-        "algorithmic_bytes": w.algo_bytes,
-        "GBps": round(w.algo_bytes / (us * 1e-6) / 1e9, 1),
-        "pct_of_hbm_peak": round(100 * w.algo_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
-        "input_copies_rotated": 8,
-    }
-    progress("2_store_4x4224_tokens: %.2f us/layer" % us)
-    del w
-    torch.cuda.empty_cache()
+    if want("2_store_4x4224_tokens"):
+        w = StoreWorkload(ops, torch, copies=8, seed=1002)
+        warm_clocks(torch, w, 1.0)
+        us = kernel_us(torch, hip, w, 3, steps, warmup)
+        rows["2_store_4x4224_tokens"] = {
+            "us_per_layer": round(us, 2),
+            "algorithmic_bytes": w.algo_bytes,
+            "GBps": round(w.algo_bytes / (us * 1e-6) / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * w.algo_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+            "input_copies_rotated": 8,
+        }
+        progress("2_store_4x4224_tokens: %.2f us/layer" % us)
+        del w
+        torch.cuda.empty_cache()
     decode_row("3_mtp_verify_4x8192_q7", [8192] * 4, 7, copies=12, seed=1003, pool_pages_per_copy=1024)
     decode_row("4_mixed_long_q7", [2048, 32768, 131072, 200000], 7, copies=3, seed=1004,
                shared_prefix_pages=1024)
-    w = PrefillWorkload(ops, torch)
-    warm_clocks(torch, w, 1.0)
-    us = kernel_us(torch, hip, w, 3, max(5, steps // 10), 2)
-    tflops = w.flops / (us * 1e-6) / 1e12
-    rows["5_prefill_4224_over_131072"] = {
-        "us_per_layer": round(us, 1),
-        "algorithmic_flops": w.flops,
-        "TFLOPs": round(tflops, 1),
-        "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
-        "mfma_utilization": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-        "dtype": "f16 MFMA (exact K codes / V nibbles), f32 accumulation",
-    }
-    del w
-    torch.cuda.empty_cache()
-    progress("5_prefill_4224_over_131072: %.1f us/layer, %.1f TFLOP/s" % (us, tflops))
+    if want("5_prefill_4224_over_131072"):
+        w = PrefillWorkload(ops, torch)
+        warm_clocks(torch, w, 1.0)
+        us = kernel_us(torch, hip, w, 3, max(5, steps // 10), 2)
+        tflops = w.flops / (us * 1e-6) / 1e12
+        rows["5_prefill_4224_over_131072"] = {
+            "us_per_layer": round(us, 1),
+            "algorithmic_flops": w.flops,
+            "TFLOPs": round(tflops, 1),
+            "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
+            "mfma_utilization": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "dtype": "f16 MFMA (exact K codes / V nibbles), f32 accumulation",
+        }
+        del w
+        torch.cuda.empty_cache()
+        progress("5_prefill_4224_over_131072: %.1f us/layer, %.1f TFLOP/s" % (us, tflops))
     decode_row("reference_shape_d256_hkv2_ctx127853_q7", [127853], 7, copies=4, seed=1007,
                hkv=2, head_dim=256)
     return rows
@@ -437,6 +446,10 @@ def main(argv=None) -> int:
 
     o = ops()
     hip = HipEvents()
+    if args.only:
+        rows = config_rows(torch, hip, o, min(args.steps, 100), min(args.warmup, 10), only=args.only)
+        print(json.dumps({"configs": rows}), flush=True)
+        return 0
     B, ctx, q_len = 4, 131072, 7
     work = DecodeWorkload(o, torch, lengths=[ctx] * B, q_len=q_len, hkv=4, head_dim=128, copies=3,
                           seed=1006, splits=args.splits)
