@@ -276,12 +276,16 @@ __device__ __forceinline__ int chunk_token(int g, int i) { return i < 4 ? 4 * g 
 
 // Direct-to-LDS loads.  K and V are read exactly once, so they carry the
 // nontemporal policy (streaming reads measured ~15% faster on MI355X); the
-// scale planes, shared by the heads of a work-group, use the default policy.
+// scale planes, shared by the heads of a work-group, and the query rows,
+// shared by the splits of a sequence, use the default policy.
 constexpr int kPolicyNontemporal = 2;
 
 __device__ __forceinline__ void dma16_nt(const void *src, lds_t *dst) {
   __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0,
                                    kPolicyNontemporal);
+}
+__device__ __forceinline__ void dma16(const void *src, lds_t *dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0, 0);
 }
 __device__ __forceinline__ void dma4(const void *src, lds_t *dst) {
   __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 4, 0, 0);
@@ -644,6 +648,9 @@ struct SplitConfig {
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
   static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
+  // The query rows of a wave's tiles are staged in its K slots 1..RK-1.
+  static_assert(!QLDS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
+                "query staging does not fit the K ring");
 };
 
 template <int D, int NT, int HKV, int NWH>
@@ -678,16 +685,15 @@ void decode_split_kernel(DecodeArgs a) {
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
 
-  // Raw query words of this wave's Q tiles, loaded before the ring's first
-  // DMAs so they do not wait behind them (vector loads complete in order).
-  uint4 qraw[NT][KS][2];
+  // Raw query words.  With Q in registers (one wave per head) they are
+  // loaded here, before the ring's first loads, so they do not wait behind
+  // them (vector loads complete in order); with Q in LDS they are staged by
+  // direct-to-LDS loads further down.
+  uint4 qraw[CFG::QLDS ? 1 : NT][KS][2];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < (CFG::QLDS ? 0 : NT); ++nt) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (CFG::QLDS) {
-      if (nt % NWH != w) continue;  // the partner wave quantizes this tile
-    }
     const int r = 16 * nt + n;
     if (r < rows) {
       const int j = r / kGqa;
@@ -754,7 +760,34 @@ void decode_split_kernel(DecodeArgs a) {
       mv[s] = issued;
     }
   };
+  // Q in LDS: this wave's query rows (its tiles nt = w, w + NWH, ...) go by
+  // direct-to-LDS loads into its K slots 1.. (filled only after the
+  // quantization), ahead of the first chunk's loads; waiting for them is then
+  // a plain count of this wave's own loads.  Rows past the last query row
+  // load row 0 and are zeroed below.
+  lds_t *qstage = kring + S::K_BYTES;
+  if constexpr (CFG::QLDS) {
+    constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt % NWH != w) continue;
+      const int ti = nt / NWH;
+#pragma unroll
+      for (int d = 0; d < 16 / RPD; ++d) {
+        const int r = 16 * nt + RPD * d + lane / (2 * D / 16);
+        const int rr = r < rows ? r : 0;
+        const int j = rr / kGqa;
+        const int qh = h * kGqa + (rr - j * kGqa);
+        const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
+                              static_cast<int64_t>(qh) * D + 8 * (lane % (2 * D / 16));
+        dma16(src, qstage + (ti * 16 + RPD * d) * 2 * D);  // shared by the splits of b: cached
+        ++issued;
+      }
+    }
+  }
+  const int q_done = issued;
   fill_slot(0);
+  if constexpr (CFG::QLDS) wait_vm(issued - q_done);
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
@@ -769,7 +802,18 @@ void decode_split_kernel(DecodeArgs a) {
       float x[KS][16];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const uint4 w0 = qraw[nt][ks][0], w1 = qraw[nt][ks][1];
+        uint4 w0, w1;
+        if constexpr (CFG::QLDS) {
+          const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
+          const bool live = 16 * nt + n < rows;
+          const v4i r0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row);
+          const v4i r1 = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16);
+          w0 = live ? make_uint4(r0[0], r0[1], r0[2], r0[3]) : make_uint4(0u, 0u, 0u, 0u);
+          w1 = live ? make_uint4(r1[0], r1[1], r1[2], r1[3]) : make_uint4(0u, 0u, 0u, 0u);
+        } else {
+          w0 = qraw[nt][ks][0];
+          w1 = qraw[nt][ks][1];
+        }
         const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -785,28 +829,16 @@ void decode_split_kernel(DecodeArgs a) {
       amax = xlane_max16_32(amax);
       const double scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
       const double inv = amax == 0.f ? 0.0 : 1.0 / scale;
-      const float inv32 = static_cast<float>(inv);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         uint32_t wq[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          // fp32 product (within 127 * 2^-23 of the float64 one); only a
-          // value whose fraction lies within 2^-12 of one half is redone in
-          // float64 as the reference computes it.
-          const float y32 = x[ks][e] * inv32;
-          const float ay = fabsf(y32);
-          const float fl = floorf(ay);
-          const float fr = ay - fl;
-          int32_t qi;
-          if (fabsf(fr - 0.5f) < 2.44140625e-4f) {
-            const double y = static_cast<double>(x[ks][e]) * inv;
-            double qv = y >= 0.0 ? floor(y + 0.5) : ceil(y - 0.5);
-            qi = static_cast<int32_t>(fmin(fmax(qv, -127.0), 127.0));
-          } else {
-            const int32_t qa = static_cast<int32_t>(fminf(fl + (fr > 0.5f ? 1.f : 0.f), 127.f));
-            qi = y32 < 0.f ? -qa : qa;
-          }
+          // float64 as the reference: |q| = floor(|x| * inv + 0.5) (the
+          // reference's ceil(y - 0.5) for y < 0 is the same magnitude).
+          const double ay = static_cast<double>(fabsf(x[ks][e])) * inv;
+          const int32_t qa = static_cast<int32_t>(fmin(floor(ay + 0.5), 127.0));
+          const int32_t qi = x[ks][e] < 0.f ? -qa : qa;
           wq[e >> 2] |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * (e & 3));
         }
         const v4i frag = (v4i){static_cast<int>(wq[0]), static_cast<int>(wq[1]), static_cast<int>(wq[2]),
@@ -828,11 +860,17 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
 
+  // The staged query rows have been read (their values are quantized).
+  if constexpr (CFG::QLDS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
   for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
 
   if constexpr (CFG::QLDS) {
-    __syncthreads();  // Q fragments and row factors visible to both waves of the head
+    // Q fragments and row factors visible to both waves of the head.  A bare
+    // barrier after the LDS writes: __syncthreads() would also wait for every
+    // ring load in flight.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       st.crow[nt] = reinterpret_cast<const __attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n];
