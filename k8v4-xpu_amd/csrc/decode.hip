@@ -640,6 +640,9 @@ struct SplitConfig {
   static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
   static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
   static constexpr int WAVE_BYTES = RK * Slot<D>::K_BYTES + RV * Slot<D>::V_BYTES;
+  // Loads issued after a chunk's V group until that chunk is consumed, in
+  // the steady state of the main loop (one K and one V group per chunk).
+  static constexpr int STEADY_AFTER = (RV - 1) * (Slot<D>::NK + Slot<D>::NVS);
   static constexpr int Q_OFF = WAVES * WAVE_BYTES;
   static constexpr int RING_BYTES = Q_OFF + HKV * Q_BYTES_PER_HEAD;
   // Partner-wave state exchange at the end (reuses the ring memory).
@@ -897,7 +900,15 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 1; s < RV; ++s)
       if (sv == s) mvs = mv[s];
-    wait_vm(issued - max(mks, mvs));
+    // Steady state: the loads issued after this chunk's V group are exactly
+    // those of the previous RV - 1 chunks; one compare picks that count.
+    {
+      const int n = issued - max(mks, mvs);
+      if (n == CFG::STEADY_AFTER)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CFG::STEADY_AFTER) : "memory");
+      else
+        wait_vm(n);
+    }
     const bool valid = (valid_mask >> sk) & 1u;
     const int tbase = 32 * (my0 + k * NWH);
     v4i sc[2][NT];
