@@ -12,10 +12,12 @@
 // multiply-add is fused.
 //
 // Mapping (MI355X): K and V of one (token, kv_head) pair are handled by the
-// same D/8 lanes, 8 consecutive dims per lane (one 16-byte load of K and one
-// of V).  Consecutive pairs are consecutive heads of a token, so a wave
+// same D/16 lanes, 16 consecutive dims per lane (two 16-byte loads of K and
+// two of V).  Consecutive pairs are consecutive heads of a token, so a wave
 // writes whole contiguous rows of a page: the store is one pass over the
-// inputs and one pass over the outputs, HBM-bound.
+// inputs and one pass over the outputs.  The per-pair work (float64 scale
+// divisions, group reductions, scale stores) is the same for every lane of a
+// group, so fewer, wider lanes per pair cut the instruction count per byte.
 #include "k8v4_common.h"
 
 namespace k8v4 {
@@ -40,22 +42,27 @@ struct StoreArgs {
   int vec_ok;  // 16-byte aligned rows: one vector load per lane
 };
 
-__device__ __forceinline__ void load8(const uint16_t *src, bool vec_ok, bool bf16, float out[8]) {
-  uint16_t h[8];
+// E consecutive fp16/bf16 values -> fp32.
+template <int E>
+__device__ __forceinline__ void load_row(const uint16_t *src, bool vec_ok, bool bf16, float out[E]) {
+  uint16_t h[E];
   if (vec_ok) {
-    const uint4 w = *reinterpret_cast<const uint4 *>(src);
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[2 * i] = static_cast<uint16_t>(words[i] & 0xFFFFu);
-      h[2 * i + 1] = static_cast<uint16_t>(words[i] >> 16);
+    for (int c = 0; c < E / 8; ++c) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(src + 8 * c);
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[8 * c + 2 * i] = static_cast<uint16_t>(words[i] & 0xFFFFu);
+        h[8 * c + 2 * i + 1] = static_cast<uint16_t>(words[i] >> 16);
+      }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = src[i];
+    for (int i = 0; i < E; ++i) h[i] = src[i];
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = half_bits_to_float(h[i], bf16);
+  for (int i = 0; i < E; ++i) out[i] = half_bits_to_float(h[i], bf16);
 }
 
 // Max / min over the LPU lanes of one (token, head) group.
@@ -72,11 +79,12 @@ __device__ __forceinline__ float group_min(float x) {
   return x;
 }
 
-// One wave handles 64/LPU (token, head) pairs; LPU = D/8 lanes per pair.
+// One wave handles 64/LPU (token, head) pairs; LPU = D/16 lanes per pair.
 template <int D>
 __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
 #pragma clang fp contract(off)
-  constexpr int LPU = D / 8;
+  constexpr int E = 16;  // dims per lane
+  constexpr int LPU = D / E;
   constexpr int UPW = kWave / LPU;
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
@@ -87,13 +95,15 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   const int64_t token = unit / a.hkv;
   const int head = static_cast<int>(unit - token * a.hkv);
 
-  float kx[8], vx[8];
-  load8(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + 8 * sub, a.vec_ok, a.bf16, kx);
-  load8(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + 8 * sub, a.vec_ok, a.bf16, vx);
+  // The slot first: its load then shares the round trip of the K/V loads.
+  const int64_t slot = a.slots[token];
+  float kx[E], vx[E];
+  load_row<E>(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, kx);
+  load_row<E>(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, vx);
 
   float amax = 0.f, lo = vx[0], hi = vx[0];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < E; ++i) {
     amax = fmaxf(amax, fabsf(kx[i]));
     lo = fminf(lo, vx[i]);
     hi = fmaxf(hi, vx[i]);
@@ -102,7 +112,6 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   lo = group_min<LPU>(lo);
   hi = group_max<LPU>(hi);
 
-  const int64_t slot = a.slots[token];
   const int64_t page = slot >= 0 ? slot / kPage : -1;
   if (!live || page < 0 || page >= a.num_pages) return;
   const int64_t row = slot - page * kPage;
@@ -118,13 +127,13 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
 
   // K: symmetric int8, scale amax/127, round half away from zero.
   const double k_scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
-  uint32_t kw[2] = {0u, 0u};
+  uint32_t kw[E / 4] = {};
   if (amax != 0.f) {
     const double inv = 1.0 / k_scale;
     const float inv32 = static_cast<float>(inv);
     const bool fast = inv32 <= 3.0e38f;  // a tiny bf16 amax overflows the fp32 reciprocal
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < E; ++i) {
       const float y32 = kx[i] * inv32;
       const float d = fabsf(y32) + 0.5f;
       float m = floorf(d);
@@ -149,22 +158,24 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   const double zero = fmin(fmax(floor(-lo_d / v_scale + 0.5), 0.0), 15.0);
   const float rs32 = static_cast<float>(1.0 / v_scale);
   const float z32 = static_cast<float>(zero);
-  uint32_t vw = 0u;
+  uint32_t vw[E / 8] = {};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < E; ++i) {
     const float y32 = vx[i] * rs32 + z32 + 0.5f;
     float q = floorf(y32);
     const float fr = y32 - q;
     if (fr < kMargin || fr > 1.f - kMargin)
       q = static_cast<float>(floor(static_cast<double>(vx[i]) / v_scale + zero + 0.5));
     q = fminf(fmaxf(q, 0.f), 15.f);
-    vw |= static_cast<uint32_t>(q) << (4 * i);
+    vw[i >> 3] |= static_cast<uint32_t>(q) << (4 * (i & 7));
   }
 
-  char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + 8 * sub;
-  *reinterpret_cast<uint2 *>(kdst) = make_uint2(kw[0], kw[1]);
-  char *vdst = reinterpret_cast<char *>(a.v_cache) + page * a.v_ps + cell * (D / 2) + 4 * sub;
-  *reinterpret_cast<uint32_t *>(vdst) = vw;
+  char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + E * sub;
+#pragma unroll
+  for (int c = 0; c < E / 16; ++c)
+    reinterpret_cast<uint4 *>(kdst)[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
+  char *vdst = reinterpret_cast<char *>(a.v_cache) + page * a.v_ps + cell * (D / 2) + (E / 2) * sub;
+  *reinterpret_cast<uint2 *>(vdst) = make_uint2(vw[0], vw[1]);
   if (sub == 0) {
     *reinterpret_cast<float *>(reinterpret_cast<char *>(a.k_scale) + page * a.ks_ps + cell * 4) =
         static_cast<float>(k_scale);
@@ -202,10 +213,10 @@ extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
   K8V4_REQUIRE(k_tok_stride >= static_cast<int64_t>(hkv) * head_dim &&
                    v_tok_stride >= static_cast<int64_t>(hkv) * head_dim,
                "k/v token stride shorter than hkv*head_dim");
-  K8V4_REQUIRE(aligned(k_cache, 8) && aligned(v_cache, 4) && aligned(k_scale, 4) &&
+  K8V4_REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 8) && aligned(k_scale, 4) &&
                    aligned(v_scale, 4) && aligned(v_zero, 4) && aligned(slot_mapping, 8),
                "cache region or slot pointer misaligned");
-  K8V4_REQUIRE(k_page_stride % 8 == 0 && v_page_stride % 4 == 0 && ks_page_stride % 4 == 0 &&
+  K8V4_REQUIRE(k_page_stride % 16 == 0 && v_page_stride % 8 == 0 && ks_page_stride % 4 == 0 &&
                    vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
                "cache page strides must keep rows aligned");
   K8V4_REQUIRE(aligned(k, 2) && aligned(v, 2), "k/v pointers misaligned");
@@ -232,7 +243,7 @@ extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
   a.bf16 = src_dtype == K8V4_BF16;
   a.vec_ok = aligned(k, 16) && aligned(v, 16) && (k_tok_stride % 8 == 0) && (v_tok_stride % 8 == 0);
 
-  const int upw = kWave / (head_dim / 8);
+  const int upw = kWave / (head_dim / 16);
   const int64_t waves = (a.units + upw - 1) / upw;
   const int64_t blocks = (waves + 3) / 4;
   K8V4_REQUIRE(blocks < (int64_t(1) << 31), "too many tokens for one launch");
