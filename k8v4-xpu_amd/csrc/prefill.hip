@@ -387,16 +387,25 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int kb = 32 * mt + 8 * j + 4 * hh;
-        const v4f ksc = *reinterpret_cast<const v4f *>(sc + kb);
+        const v4f ksc = *reinterpret_cast<const v4f *>(sc + 32 * mt + 8 * j + 4 * hh);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = S[mt][4 * j + i] * ksc[i];
-          if (masked) x = p * 64 + kb + i < lim ? x : -INFINITY;
-          S[mt][4 * j + i] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int i = 0; i < 4; ++i) S[mt][4 * j + i] *= ksc[i];
       }
+    // The causal mask touches only the last pages of a block: a uniform
+    // branch, so the common pages carry no per-score compare and select.
+    if (__builtin_expect(masked, 0)) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (p * 64 + 32 * mt + 8 * j + 4 * hh + i >= lim) S[mt][4 * j + i] = -INFINITY;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, S[mt][e]);
     {
       auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
