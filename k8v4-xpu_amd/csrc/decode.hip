@@ -75,6 +75,7 @@ struct DecodeArgs {
   int64_t split_floats;  // floats of one split's state
   int grid;              // number of split work-groups (the plan's G)
   int min_pages;
+  int merge_cs;  // column slices per output row in the merge kernel
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -1022,12 +1023,14 @@ void decode_split_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------ merge kernel
-// One 256-thread work-group per output row (token, query head).  Thread t
-// owns 16-byte column t % (D/4) of the row and the splits s = t / (D/4) +
-// k * (256 / (D/4)).  It loads the (m, l, O) of up to MU of its splits at once
-// and folds them online (running max, rescaled sums), so the whole merge is
-// one round trip to memory; the per-thread partial states are then combined
-// in LDS with the same rescaling.
+// One 256-thread work-group per (output row, column slice): the D/4 16-byte
+// columns of a row (token, query head) are cut into `merge_cs` slices of
+// VPR = D/4/merge_cs columns, so a row whose sequence has many splits is
+// spread over several work-groups.  Thread t owns column t % VPR of the
+// slice and the splits s = t / VPR + k * SPI (SPI = 256 / VPR).  It loads the
+// (m, l, O) of up to MU of its splits at once and folds them online (running
+// max, rescaled sums), one round trip per MU splits; the per-thread partial
+// states are then combined in LDS with the same rescaling.
 
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
   if (dtype == K8V4_F32)
@@ -1040,13 +1043,14 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
 
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int VPR = D / 4;       // 16-byte columns per row state
-  constexpr int SPI = 256 / VPR;   // split groups per work-group
-  constexpr int MU = 8;            // splits loaded together by one thread
+  constexpr int MU = 8;  // splits loaded together by one thread
+  const int VPR = (D / 4) / a.merge_cs;  // 16-byte columns per slice (>= 8)
+  const int SPI = 256 / VPR;             // split groups per work-group (<= 32)
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int hq = kGqa * a.hkv;
-  const int row_id = blockIdx.x;
+  const int row_id = blockIdx.x / a.merge_cs;
+  const int slice = blockIdx.x - row_id * a.merge_cs;
   const int qh = row_id % hq;
   const int tok = row_id / hq;  // b * q_len + j
   const int j = tok % a.q_len;
@@ -1059,16 +1063,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   const SplitRange sr = plan_locate(a, P, lane, b, -1);
   const int first = sr.first, count = sr.b < 0 ? 0 : sr.count;
 
-  const int64_t o_off = static_cast<int64_t>(h * rows + r) * D;
+  const int col = tid % VPR, sg = tid / VPR;
+  const int dcol = 4 * (slice * VPR + col);  // first dim of this thread's column
+  const int64_t o_off = static_cast<int64_t>(h * rows + r) * D + dcol;
   const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D + h * rows + r;
   const int64_t l_off = m_off + a.hkv * rows;
   const float *ws = a.ws + static_cast<int64_t>(first) * a.split_floats;
 
-  __shared__ float red_m[SPI];
-  __shared__ float red_l[SPI];
-  __shared__ v4f red_o[SPI][VPR];
+  __shared__ float red_m[32];
+  __shared__ float red_l[32];
+  __shared__ v4f red_o[256];  // [SPI][VPR]
 
-  const int col = tid % VPR, sg = tid / VPR;
   float M = -INFINITY, lacc = 0.f;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = sg; s0 < count; s0 += MU * SPI) {
@@ -1084,7 +1089,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         const float *st = ws + static_cast<int64_t>(s) * a.split_floats;
         ms[u] = __builtin_nontemporal_load(st + m_off);
         ls[u] = __builtin_nontemporal_load(st + l_off);
-        os[u] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(st + o_off + 4 * col));
+        os[u] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(st + o_off));
       }
     }
     float mn = M;
@@ -1103,7 +1108,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
       M = mn;
     }
   }
-  red_o[sg][col] = acc;
+  red_o[tid] = acc;
   if (col == 0) {
     red_m[sg] = M;
     red_l[sg] = lacc;
@@ -1111,30 +1116,23 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
   __syncthreads();
   if (tid >= VPR) return;
   float Mg = -INFINITY;
-#pragma unroll
   for (int g2 = 0; g2 < SPI; ++g2) Mg = fmaxf(Mg, red_m[g2]);
   float l = 0.f;
   v4f o = {0.f, 0.f, 0.f, 0.f};
   if (Mg != -INFINITY) {
-#pragma unroll
     for (int g2 = 0; g2 < SPI; ++g2) {
       const float mg = red_m[g2];
       const float w = mg == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg - Mg);
       l += w * red_l[g2];
-      o += w * red_o[g2][tid];
+      o += w * red_o[g2 * VPR + tid];
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * tid;
+  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + dcol;
 #pragma unroll
   for (int e = 0; e < 4; ++e) store_out(a.out, a.out_dtype, ob + e, o[e] * inv);
 }
 
-// ------------------------------------------------------------ host side
-
-
-// Waves per KV head: two (two waves per SIMD) when the state fits 256
-// registers per wave, else one.
 template <int D, int NT>
 constexpr int waves_per_head() { return (D == 128 && NT <= 3) ? 2 : 1; }
 
@@ -1259,6 +1257,18 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
   a.split_floats = split_floats;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
+  // Column slices per output row: enough that a merge thread folds at most
+  // 16 splits of a sequence with the average split count G / batch (one long
+  // sequence can own all G splits); one slice per row otherwise, since every
+  // extra work-group repeats the plan.
+  {
+    const int vpr = head_dim / 4;
+    const int64_t avg = (a.grid + batch - 1) / batch;
+    int cs = 1;
+    while (vpr / cs > 8 && (256 / (vpr / cs)) * 16 < avg) cs *= 2;
+    a.merge_cs = cs;
+  }
+  K8V4_REQUIRE(batch * q_len * kGqa * hkv * a.merge_cs <= INT32_MAX, "batch too large for one merge launch");
   a.out = out;
   a.out_dtype = out_dtype;
   a.out_tok_stride = out_tok_stride;
@@ -1282,7 +1292,7 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
     }
   }
   if (!(stages & 2)) return K8V4_OK;
-  const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv));
+  const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv * a.merge_cs));
   if (head_dim == 128)
     decode_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
   else
