@@ -89,24 +89,20 @@ struct Tile {
   // one per-lane base plus a compile-time offset.
   static constexpr int KROW = 2 * D + 16;            // K row: D fp16 codes + 16 B (8 rows hit 8 bank groups)
   static constexpr int K_BYTES = 64 * KROW;
-  static constexpr int V_OFF = K_BYTES;              // V^T: row d = 64 keys fp16 (8-byte chunks XOR d%16)
-  static constexpr int VBLK = 16 * 128 + 8;          // 16 rows, then 8 B of padding
-  static constexpr int S_OFF = V_OFF + (D / 16) * VBLK;  // ksc[64] | vs[64] | vz[64] floats
+  static constexpr int V_OFF = K_BYTES;              // V^T: row d = 64 keys fp16
+  static constexpr int VROW = 128 + 8;               // V^T row: 64 keys + 8 B (32 rows hit all 64 banks)
+  static constexpr int S_OFF = V_OFF + D * VROW;     // ksc[64] | vs[64] | vz[64] floats
   static constexpr int BUF = S_OFF + 768;
-  // Staging of the next page's raw codes: [64][D] K | [64][D/2] V (its scale
-  // planes go straight into the S area of the ring buffer they belong to).
+  // Staging of the next page's raw codes: [64][D] K | V as 16-byte pieces
+  // ordered [part q][key parity][key pair] (its scale planes go straight into
+  // the S area of the ring buffer they belong to).
   static constexpr int SV_OFF = 64 * D;
   static constexpr int STAGE = SV_OFF + 32 * D;
   static constexpr int KDMA = D / 16;                 // 1 KB K pieces per page (one DMA each)
   static constexpr int VDMA = D / 32;                 // 1 KB V pieces per page
   static constexpr int KCHUNKS = 4 * D;               // 16-byte K code chunks per page
-  static constexpr int VITEMS = 2 * D;                // (key pair, 8-byte group) V items per page
+  static constexpr int VITEMS = 2 * D;                // (part, half, key pair) V items per page
 };
-
-template <int D>
-__device__ __forceinline__ int vt_offset(int d, int chunk) {
-  return (d >> 4) * Tile<D>::VBLK + (d & 15) * 128 + ((chunk ^ (d & 15)) * 8);
-}
 
 typedef const __attribute__((address_space(4))) int32_t *const_i32_ptr;
 
@@ -152,9 +148,9 @@ __device__ __forceinline__ void stage_page(const PrefillArgs &a, int p, int h, i
   for (int j = 0; j < (T::VDMA + T::NW - 1) / T::NW; ++j) {
     const int idx = T::NW * j + wave;
     if (idx < T::VDMA) {
-      const int c = 64 * idx + lane;
-      const int key = c / (D / 32), part = c % (D / 32);
-      dma16(vb + static_cast<int64_t>(key) * a.hkv * (D / 2) + part * 16, stage + T::SV_OFF + 1024 * idx);
+      // piece q = idx of key 2 * (lane % 32) + lane / 32
+      const int key = 2 * (lane & 31) + (lane >> 5);
+      dma16(vb + static_cast<int64_t>(key) * a.hkv * (D / 2) + idx * 16, stage + T::SV_OFF + 1024 * idx);
     }
   }
   if (wave < 3) {
@@ -199,25 +195,27 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
     *reinterpret_cast<uint4 *>(row + 32 * part) = c0;
     *reinterpret_cast<uint4 *>(row + 32 * part + 16) = c1;
   }
+  // V: item (part q, half, key pair p) reads the 16-byte pieces of keys 2p and
+  // 2p + 1 (the half's 8 bytes are dims 32q + 16 half .. + 15) and writes one
+  // word (both keys) into each of those 16 V^T rows.  Lanes run over key
+  // pairs, so the piece reads are consecutive and the 64 row writes of one
+  // instruction land in 64 distinct banks (rows 16 apart are 32 banks apart).
 #pragma unroll
   for (int j = 0; j < (T::VITEMS + T::THREADS - 1) / T::THREADS; ++j) {
     const int it = tid + T::THREADS * j;
     if (it >= T::VITEMS) break;
-    const int pair = it / (D / 16), grp = it % (D / 16);
-    const uint2 v0 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair) * (D / 2) + 8 * grp);
-    const uint2 v1 = *reinterpret_cast<const uint2 *>(stage + T::SV_OFF + (2 * pair + 1) * (D / 2) + 8 * grp);
-    const int chunk = pair >> 1, word = (pair & 1) * 4;
+    const int q = it >> 6, half = (it >> 5) & 1, pair = it & 31;
+    const uint4 e4 = *reinterpret_cast<const uint4 *>(stage + T::SV_OFF + (q * 64 + pair) * 16);
+    const uint4 o4 = *reinterpret_cast<const uint4 *>(stage + T::SV_OFF + (q * 64 + 32 + pair) * 16);
+    const uint32_t ev[2] = {half ? e4.z : e4.x, half ? e4.w : e4.y};
+    const uint32_t od[2] = {half ? o4.z : o4.x, half ? o4.w : o4.y};
+    char *vrow = buf + T::V_OFF + (32 * q + 16 * half) * T::VROW + 4 * pair;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      const uint32_t w0 = b < 4 ? v0.x : v0.y;
-      const uint32_t w1 = b < 4 ? v1.x : v1.y;
       const uint32_t sel = 0x0C000C00u | ((4u + (b & 3)) << 16) | (b & 3);
-      const uint32_t x = __builtin_amdgcn_perm(w1, w0, sel);  // byte b of both keys, one per 16-bit half
-      const int d = 16 * grp + 2 * b;
-      char *ve = buf + T::V_OFF + vt_offset<D>(d, chunk) + word;
-      char *vo = buf + T::V_OFF + vt_offset<D>(d + 1, chunk) + word;
-      *reinterpret_cast<uint32_t *>(ve) = x & kEvenNib;
-      *reinterpret_cast<uint32_t *>(vo) = x & kOddNib;
+      const uint32_t x = __builtin_amdgcn_perm(od[b >> 2], ev[b >> 2], sel);  // byte b of both keys
+      *reinterpret_cast<uint32_t *>(vrow + (2 * b) * T::VROW) = x & kEvenNib;
+      *reinterpret_cast<uint32_t *>(vrow + (2 * b + 1) * T::VROW) = x & kOddNib;
     }
   }
   if (tid < 64) {
@@ -345,14 +343,10 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
   float m_run = -INFINITY, lsum = 0.f, corr = 0.f;
 
   // Per-lane LDS read bases.  K: key 32*mt + r32, dims 16*ds + 8*hh.  V^T:
-  // dim 32*dt + r32, key chunks c = 4*s + hh (+2) of the s-th 16-key step.
+  // dim 32*dt + r32, 8-byte key chunks c = 4*s + 2*u + hh of the s-th 16-key
+  // step (u = 0, 1); everything else is a compile-time offset.
   const int k_base = r32 * T::KROW + 16 * hh;
-  int v_off[8];
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      v_off[2 * s + u] = vt_offset<D>(r32, 4 * s + 2 * u + hh);
+  const int v_base = T::V_OFF + r32 * T::VROW + 8 * hh;
 
   stage_page<D>(a, p_lo, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
   wait_dma();
@@ -443,14 +437,14 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
       }
 
     // ---- O^T += V^T P'^T (16-key steps st = 2*mt + j/2)
-    const char *vbase = buf + T::V_OFF;
+    const char *vbase = buf + v_base;
 #pragma unroll
     for (int dt = 0; dt < T::DT; ++dt) {
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const int blk = 2 * dt * T::VBLK;
-        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + blk + v_off[2 * st]);
-        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + blk + v_off[2 * st + 1]);
+        const int blk = 32 * dt * T::VROW + 32 * st;
+        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + blk);
+        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + blk + 16);
         const v8h vf = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
         O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[st], O[dt], 0, 0, 0);
       }
