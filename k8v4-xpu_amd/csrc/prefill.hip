@@ -89,8 +89,13 @@ struct Tile {
   // one per-lane base plus a compile-time offset.
   static constexpr int KROW = 2 * D + 16;            // K row: D fp16 codes + 16 B (8 rows hit 8 bank groups)
   static constexpr int K_BYTES = 64 * KROW;
-  static constexpr int V_OFF = K_BYTES;              // V^T: row d = 64 keys fp16
-  static constexpr int VROW = 128 + 8;               // V^T row: 64 keys + 8 B (32 rows hit all 64 banks)
+  // V^T: row d = the 64 keys' fp16 values, key k at position k with bits 2
+  // and 3 swapped, so the 8 keys one lane feeds to a 16-key MFMA step sit in
+  // 16 contiguous bytes.  Rows padded to 144 B (D = 128: one aligned 16-byte
+  // read per operand, 16 rows hit all 64 banks) or 136 B (D = 256, where the
+  // LDS is full: two 8-byte reads).
+  static constexpr int V_OFF = K_BYTES;
+  static constexpr int VROW = D == 128 ? 144 : 136;
   static constexpr int S_OFF = V_OFF + D * VROW;     // ksc[64] | vs[64] | vz[64] floats
   static constexpr int BUF = S_OFF + 768;
   // Staging of the next page's raw codes: [64][D] K | V as 16-byte pieces
@@ -209,7 +214,9 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
     const uint4 o4 = *reinterpret_cast<const uint4 *>(stage + T::SV_OFF + (q * 64 + 32 + pair) * 16);
     const uint32_t ev[2] = {half ? e4.z : e4.x, half ? e4.w : e4.y};
     const uint32_t od[2] = {half ? o4.z : o4.x, half ? o4.w : o4.y};
-    char *vrow = buf + T::V_OFF + (32 * q + 16 * half) * T::VROW + 4 * pair;
+    const int kp = 2 * pair;  // even key; its column swaps bits 2 and 3
+    const int col = (kp & ~12) | ((kp & 4) << 1) | ((kp & 8) >> 1);
+    char *vrow = buf + T::V_OFF + (32 * q + 16 * half) * T::VROW + 2 * col;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const uint32_t sel = 0x0C000C00u | ((4u + (b & 3)) << 16) | (b & 3);
@@ -343,10 +350,11 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
   float m_run = -INFINITY, lsum = 0.f, corr = 0.f;
 
   // Per-lane LDS read bases.  K: key 32*mt + r32, dims 16*ds + 8*hh.  V^T:
-  // dim 32*dt + r32, 8-byte key chunks c = 4*s + 2*u + hh of the s-th 16-key
-  // step (u = 0, 1); everything else is a compile-time offset.
+  // dim 32*dt + r32, columns 16*s + 8*hh .. + 7 of the s-th 16-key step (keys
+  // 16s + 4hh + i and 16s + 8 + 4hh + i); everything else is a compile-time
+  // offset.
   const int k_base = r32 * T::KROW + 16 * hh;
-  const int v_base = T::V_OFF + r32 * T::VROW + 8 * hh;
+  const int v_base = T::V_OFF + r32 * T::VROW + 16 * hh;
 
   stage_page<D>(a, p_lo, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
   wait_dma();
@@ -443,9 +451,14 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int blk = 32 * dt * T::VROW + 32 * st;
-        const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + blk);
-        const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + blk + 16);
-        const v8h vf = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        v8h vf;
+        if constexpr (T::VROW % 16 == 0) {
+          vf = *reinterpret_cast<const v8h *>(vbase + blk);
+        } else {
+          const uint2 lo = *reinterpret_cast<const uint2 *>(vbase + blk);
+          const uint2 hi = *reinterpret_cast<const uint2 *>(vbase + blk + 8);
+          vf = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
         O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[st], O[dt], 0, 0, 0);
       }
     }
