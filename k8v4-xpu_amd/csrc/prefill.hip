@@ -370,16 +370,16 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
 
     // ---- S^T = K Q^T for the 64 keys of page p: lane (r, hh) reg 4j+i of
     // tile mt holds key 32*mt + 8*j + 4*hh + i of row r.
-    v16f S[2];
+    // The two 32-key tiles alternate, so consecutive MFMAs never wait on
+    // each other's accumulator.
+    v16f S[2] = {(v16f)0.f, (v16f)0.f};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      S[mt] = (v16f)0.f;
+    for (int ds = 0; ds < T::DS; ++ds)
 #pragma unroll
-      for (int ds = 0; ds < T::DS; ++ds) {
+      for (int mt = 0; mt < 2; ++mt) {
         const v8h kf = *reinterpret_cast<const v8h *>(buf + k_base + 32 * mt * T::KROW + 32 * ds);
         S[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], S[mt], 0, 0, 0);
       }
-    }
 
     // ---- scaled scores, masks, lazy max
     const float *sc = reinterpret_cast<const float *>(buf + T::S_OFF);
@@ -444,12 +444,13 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
         }
       }
 
-    // ---- O^T += V^T P'^T (16-key steps st = 2*mt + j/2)
+    // ---- O^T += V^T P'^T (16-key steps st = 2*mt + j/2; the DT output tiles
+    // alternate, so consecutive MFMAs are independent)
     const char *vbase = buf + v_base;
 #pragma unroll
-    for (int dt = 0; dt < T::DT; ++dt) {
+    for (int st = 0; st < 4; ++st) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
+      for (int dt = 0; dt < T::DT; ++dt) {
         const int blk = 32 * dt * T::VROW + 32 * st;
         v8h vf;
         if constexpr (T::VROW % 16 == 0) {
