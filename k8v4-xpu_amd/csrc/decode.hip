@@ -437,21 +437,23 @@ __device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const
       kf[ml][ks] = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
           kslot + t * D + 16 * (c ^ kswz<D>(t)));
     }
+  // k-step outermost: the 2 * NT score tiles are independent accumulators,
+  // so consecutive MFMAs never wait on each other.
 #pragma unroll
   for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      v4i acc = {0, 0, 0, 0};
+    for (int nt = 0; nt < NT; ++nt) sc[ml][nt] = (v4i){0, 0, 0, 0};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        v4i qf;
-        if constexpr (QLDS)
-          qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
-        else
-          qf = st.qb[nt][ks];
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, acc, 0, 0, 0);
-      }
-      sc[ml][nt] = acc;
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      v4i qf;
+      if constexpr (QLDS)
+        qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
+      else
+        qf = st.qb[nt][ks];
+#pragma unroll
+      for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
     }
 }
 
