@@ -73,7 +73,11 @@ class Scratch:
 
 
 def scratch_key(device: torch.device, layout: PageLayout) -> tuple[str, int | None, int, int]:
-    return (device.type, device.index, layout.hkv, layout.head_dim)
+    device = torch.device(device)
+    index = device.index
+    if index is None and device.type == "cuda":
+        index = torch.cuda.current_device()  # "cuda" and "cuda:N" name the same slot
+    return (device.type, index, layout.hkv, layout.head_dim)
 
 
 def ensure_scratch(
