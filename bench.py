@@ -13,10 +13,13 @@ non-contiguous block tables.  Prints ONE JSON line:
   the stream it runs on (the library records one between its two kernels),
   against the 8 TB/s HBM peak; ``traffic`` comes from the committed
   rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
-* ``cpu_baseline``: the float64 oracle (oracle/attention.py) on one of the
-  four sequences, single-threaded, on this host;
+* ``cpu_baseline``: the float64 oracle (oracle/attention.py) over the whole
+  headline step, single-threaded, on this host;
+* ``step_graph_us`` and the configs' ``graph_us_*``: per-launch time from HIP
+  graphs of back-to-back launches replayed between two events (median and
+  min of several replays), which leaves out the host launch cost;
 * ``configs``: microseconds per layer of the other workloads (store, short
-  decode, MTP verify, mixed long context, the D=256 per-rank shape).
+  decode, MTP verify, mixed long context, prefill, the D=256 per-rank shape).
 
 Inputs are synthetic: fp16 N(0,1) K/V quantized into the cache by the store
 kernel, fp16 N(0,1) queries.  Several copies of each cache are rotated from
@@ -295,6 +298,37 @@ def kernel_us(torch, hip, work, stages, steps, warmup):
     return us
 
 
+def graph_us(torch, work, launches=20, replays=10, reps=7):
+    """Per-launch microseconds from a HIP graph of ``launches`` back-to-back
+    launches (rotating the work's input copies), replayed ``replays`` times
+    between two events, ``reps`` times: (median, min).  No host launch cost."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(launches):
+            work.launch(i)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(launches):
+            work.launch(i)
+    for _ in range(3):
+        graph.replay()
+    synchronize(torch)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per = []
+    for _ in range(reps):
+        a.record()
+        for _ in range(replays):
+            graph.replay()
+        b.record()
+        synchronize(torch)
+        per.append(1e3 * a.elapsed_time(b) / (replays * launches))
+    del graph
+    per.sort()
+    return per[len(per) // 2], per[0]
+
+
 def copy_peak_gbs(torch, hip, nbytes=1 << 30, reps=20):
     """Read+write GB/s of a plain device copy (the calibration kernel for byte counters)."""
     src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
@@ -378,8 +412,11 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
                            copies=copies, seed=seed, **kw)
         warm_clocks(torch, w, 1.0)
         us = kernel_us(torch, hip, w, 3, steps, warmup)
+        g_med, g_min = graph_us(torch, w)
         rows[name] = {
             "us_per_layer": round(us, 2),
+            "graph_us_median": round(g_med, 2),
+            "graph_us_min": round(g_min, 2),
             "split_kernel_us": round(kernel_us(torch, hip, w, 1, steps, warmup), 2),
             "merge_kernel_us": round(kernel_us(torch, hip, w, 2, steps, warmup), 2),
             "kv_bytes": w.kv_bytes,
@@ -396,8 +433,11 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
         w = StoreWorkload(ops, torch, copies=8, seed=1002)
         warm_clocks(torch, w, 1.0)
         us = kernel_us(torch, hip, w, 3, steps, warmup)
+        g_med, g_min = graph_us(torch, w)
         rows["2_store_4x4224_tokens"] = {
             "us_per_layer": round(us, 2),
+            "graph_us_median": round(g_med, 2),
+            "graph_us_min": round(g_min, 2),
             "algorithmic_bytes": w.algo_bytes,
             "GBps": round(w.algo_bytes / (us * 1e-6) / 1e9, 1),
             "pct_of_hbm_peak": round(100 * w.algo_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
@@ -413,9 +453,12 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
         w = PrefillWorkload(ops, torch)
         warm_clocks(torch, w, 1.0)
         us = kernel_us(torch, hip, w, 3, max(5, steps // 10), 2)
+        g_med, g_min = graph_us(torch, w, launches=2, replays=2, reps=3)
         tflops = w.flops / (us * 1e-6) / 1e12
         rows["5_prefill_4224_over_131072"] = {
             "us_per_layer": round(us, 1),
+            "graph_us_median": round(g_med, 1),
+            "graph_us_min": round(g_min, 1),
             "algorithmic_flops": w.flops,
             "TFLOPs": round(tflops, 1),
             "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
@@ -458,6 +501,7 @@ def main(argv=None) -> int:
     ms_per_step = 1e3 * wall / args.steps
     gbs = work.kv_bytes / (wall / args.steps) / 1e9
 
+    step_graph = graph_us(torch, work)
     split_us = kernel_us(torch, hip, work, 1, args.steps, args.warmup)
     merge_us = kernel_us(torch, hip, work, 2, args.steps, args.warmup)
     achieved = work.kv_bytes / (split_us * 1e-6) / 1e9
@@ -485,6 +529,8 @@ def main(argv=None) -> int:
             "parallelism": "single GPU",
         },
         "us_per_layer": round(1e3 * ms_per_step, 2),
+        "step_graph_us": {"median": round(step_graph[0], 2), "min": round(step_graph[1], 2),
+                          "launches": "hipGraph of 20 steps, 10 replays x 7"},
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "roofline": {
             "kernel": "decode_split_kernel",
