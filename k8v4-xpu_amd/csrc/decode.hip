@@ -29,7 +29,7 @@
 //    16 n * 2^-24 after one AND), the V scale multiplies P and the zero point
 //    is one extra MFMA per tile (sum_t p_t s_t z_t), removed at the end;
 //    P.V and the row sums on v_mfma_f32_16x16x32_f16 with fp32 accumulation.
-//  * Each split writes (m, l, unnormalized O) for its live rows only; a small
+//  * Each split writes (m, l, O / l in fp16) for its live rows only; a small
 //    merge kernel combines the splits of each output row.
 #include "k8v4_common.h"
 
@@ -43,6 +43,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 // Lazy-rescale threshold (log2 units): a probability stays <= 2^4 before the
@@ -71,8 +72,8 @@ struct DecodeArgs {
   int batch;
   int q_len;
   int hkv;
-  float *ws;
-  int64_t split_floats;  // floats of one split's state
+  char *ws;
+  int64_t split_bytes;  // bytes of one split's state
   int grid;              // number of split work-groups (the plan's G)
   int min_pages;
   int merge_cs;  // column slices per output row in the merge kernel
@@ -416,6 +417,7 @@ struct WaveState {
   float crow[NT];   // q_scale * log2(e) / sqrt(D), > 0
   int lim[NT];      // causal end of this lane's row (S layout)
   float m_run[NT];  // running max, log2 domain (S layout)
+  float thr[NT];    // (m_run + threshold) / crow: a raw score above it moves m_run
   v4f lsum[NT];     // row sums (O layout, rows 4g+i)
   v4f corr[NT];     // sum of P * v_scale * v_zero per row (O layout)
   v4f O[NT][DG][8]; // unnormalized output (O layout)
@@ -487,7 +489,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
   }
   // ---- scores, chunk max, lazy rescale
   float t[2][NT][4];
-  float mc[NT];
+  float lmx[NT];  // this lane's largest score of each row tile
   bool grow = false;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -510,15 +512,18 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
     for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mx = fmaxf(mx, t[ml][nt][i]);
-    mc[nt] = xlane_max16_32(mx) * st.crow[nt];
-    grow |= mc[nt] > st.m_run[nt] + kRescaleThreshold;
+    lmx[nt] = mx;
+    // A row's largest score passes the threshold exactly when one of its four
+    // lanes' does, so the cross-lane max is only taken on a rescale.
+    grow |= mx > st.thr[nt];
   }
   if (__ballot(grow)) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float mnew = fmaxf(st.m_run[nt], mc[nt]);
+      const float mnew = fmaxf(st.m_run[nt], xlane_max16_32(lmx[nt]) * st.crow[nt]);
       const float alpha = st.m_run[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m_run[nt] - mnew);
       st.m_run[nt] = mnew;
+      st.thr[nt] = (mnew + kRescaleThreshold) / st.crow[nt];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float ai = __shfl(alpha, 4 * g + i, kWave);
@@ -886,6 +891,7 @@ void decode_split_kernel(DecodeArgs a) {
     st.lsum[nt] = (v4f){0.f, 0.f, 0.f, 0.f};
     st.corr[nt] = (v4f){0.f, 0.f, 0.f, 0.f};
     st.m_run[nt] = -INFINITY;
+    st.thr[nt] = -INFINITY;
 #pragma unroll
     for (int dg = 0; dg < DG; ++dg)
 #pragma unroll
@@ -998,9 +1004,14 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
 
-  // Split state: O rows (lane rows 16nt+4g+i, dims dg*128+8n+j), m, l.
-  float *base = a.ws + static_cast<int64_t>(blockIdx.x) * a.split_floats;
-  float *mbase = base + static_cast<int64_t>(HKV) * rows * D;
+  // Split state: O normalized by the split's row sum, times 1/4, in fp16
+  // (lane rows 16nt+4g+i, dims dg*128+8n+j: one 16-byte store per row and
+  // dim group), then m and l in fp32.  A dequantized V value is at most
+  // 15 * (65504 * 2 / 15) in magnitude, so a quarter of any average of them
+  // is a finite fp16; the merge multiplies by 4 again (exact).
+  char *base = a.ws + static_cast<int64_t>(blockIdx.x) * a.split_bytes;
+  _Float16 *obase = reinterpret_cast<_Float16 *>(base);
+  float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(HKV) * rows * D * 2);
   float *lbase = mbase + HKV * rows;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -1008,15 +1019,18 @@ void decode_split_kernel(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * nt + 4 * g + i;
       if (r < rows) {
+        const float l = st.lsum[nt][i];
+        const float f = l > 0.f ? 0.25f / l : 0.f;
 #pragma unroll
         for (int dg = 0; dg < DG; ++dg) {
-          float *dst = base + static_cast<int64_t>(h * rows + r) * D + dg * 128 + 8 * n;
-          *reinterpret_cast<v4f *>(dst) =
-              (v4f){st.O[nt][dg][0][i], st.O[nt][dg][1][i], st.O[nt][dg][2][i], st.O[nt][dg][3][i]};
-          *reinterpret_cast<v4f *>(dst + 4) =
-              (v4f){st.O[nt][dg][4][i], st.O[nt][dg][5][i], st.O[nt][dg][6][i], st.O[nt][dg][7][i]};
+          _Float16 *dst = obase + static_cast<int64_t>(h * rows + r) * D + dg * 128 + 8 * n;
+          const v8h o = {static_cast<_Float16>(st.O[nt][dg][0][i] * f), static_cast<_Float16>(st.O[nt][dg][1][i] * f),
+                         static_cast<_Float16>(st.O[nt][dg][2][i] * f), static_cast<_Float16>(st.O[nt][dg][3][i] * f),
+                         static_cast<_Float16>(st.O[nt][dg][4][i] * f), static_cast<_Float16>(st.O[nt][dg][5][i] * f),
+                         static_cast<_Float16>(st.O[nt][dg][6][i] * f), static_cast<_Float16>(st.O[nt][dg][7][i] * f)};
+          *reinterpret_cast<v8h *>(dst) = o;
         }
-        if (n == 0) lbase[h * rows + r] = st.lsum[nt][i];
+        if (n == 0) lbase[h * rows + r] = l;
       }
     }
     const int r = 16 * nt + n;
@@ -1025,8 +1039,8 @@ void decode_split_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------ merge kernel
-// One 256-thread work-group per (output row, column slice): the D/4 16-byte
-// columns of a row (token, query head) are cut into `merge_cs` slices of
+// One 256-thread work-group per (output row, column slice): the D/4 columns
+// (four dims each) of a row (token, query head) are cut into `merge_cs` slices of
 // VPR = D/4/merge_cs columns, so a row whose sequence has many splits is
 // spread over several work-groups.  Thread t owns column t % VPR of the
 // slice and the splits s = t / VPR + k * SPI (SPI = 256 / VPR).  It loads the
@@ -1067,10 +1081,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
   const int col = tid % VPR, sg = tid / VPR;
   const int dcol = 4 * (slice * VPR + col);  // first dim of this thread's column
-  const int64_t o_off = static_cast<int64_t>(h * rows + r) * D + dcol;
-  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D + h * rows + r;
-  const int64_t l_off = m_off + a.hkv * rows;
-  const float *ws = a.ws + static_cast<int64_t>(first) * a.split_floats;
+  // Byte offsets inside one split state (layout written by the split kernel).
+  const int64_t o_off = (static_cast<int64_t>(h * rows + r) * D + dcol) * 2;
+  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (h * rows + r) * 4;
+  const int64_t l_off = m_off + a.hkv * rows * 4;
+  const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
 
   __shared__ float red_m[32];
   __shared__ float red_l[32];
@@ -1088,10 +1103,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
       ls[u] = 0.f;
       os[u] = (v4f){0.f, 0.f, 0.f, 0.f};
       if (s < count) {
-        const float *st = ws + static_cast<int64_t>(s) * a.split_floats;
-        ms[u] = __builtin_nontemporal_load(st + m_off);
-        ls[u] = __builtin_nontemporal_load(st + l_off);
-        os[u] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(st + o_off));
+        const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
+        // Default-policy loads: the states were written by the split kernel
+        // just before, and nontemporal loads of them measured slower.
+        ms[u] = *reinterpret_cast<const float *>(st + m_off);
+        ls[u] = *reinterpret_cast<const float *>(st + l_off);
+        const v4h oh = *reinterpret_cast<const v4h *>(st + o_off);
+        os[u] = __builtin_convertvector(oh, v4f);
       }
     }
     float mn = M;
@@ -1103,9 +1121,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
       acc *= c;
 #pragma unroll
       for (int u = 0; u < MU; ++u) {
-        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn);
-        lacc += w * ls[u];
-        acc += w * os[u];
+        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
+        lacc += w;
+        acc += (4.f * w) * os[u];
       }
       M = mn;
     }
@@ -1149,8 +1167,9 @@ void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
   }
 }
 
-int64_t split_state_floats(int hkv, int q_len, int head_dim) {
-  return static_cast<int64_t>(hkv) * q_len * kGqa * (head_dim + 2);
+// One split's state: per KV head and query row, D fp16 outputs, then m and l.
+int64_t split_state_bytes(int hkv, int q_len, int head_dim) {
+  return static_cast<int64_t>(hkv) * q_len * kGqa * (2 * head_dim + 8);
 }
 
 // Split work-groups for one call: about one per CU (a work-group is one wave
@@ -1175,7 +1194,7 @@ extern "C" int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width,
       !supported_dim(head_dim))
     return -1;
   const int64_t g = choose_grid(batch, table_width, pages_per_block, hkv, INT64_MAX, num_splits);
-  return g * split_state_floats(hkv, q_len, head_dim) * 4;
+  return g * split_state_bytes(hkv, q_len, head_dim);
 }
 
 namespace k8v4 {
@@ -1220,13 +1239,13 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
   K8V4_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
   if (visible_lens) K8V4_REQUIRE(vis_stride >= 1 + q_len, "visible_lens [B, 1+q_len]");
 
-  const int64_t split_floats = split_state_floats(hkv, q_len, head_dim);
-  const int64_t ws_splits = workspace_bytes / (split_floats * 4);
+  const int64_t split_bytes = split_state_bytes(hkv, q_len, head_dim);
+  const int64_t ws_splits = workspace_bytes / split_bytes;
   const int64_t grid = choose_grid(batch, table_width, pages_per_block, hkv, ws_splits, num_splits);
   if (grid > ws_splits) {
     set_error("K8/V4 workspace holds %lld split states, the batch needs at least %lld (%lld bytes each)",
               static_cast<long long>(ws_splits), static_cast<long long>(grid),
-              static_cast<long long>(split_floats * 4));
+              static_cast<long long>(split_bytes));
     return K8V4_ERR_WORKSPACE;
   }
 
@@ -1255,8 +1274,8 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
   a.batch = static_cast<int>(batch);
   a.q_len = q_len;
   a.hkv = hkv;
-  a.ws = static_cast<float *>(workspace);
-  a.split_floats = split_floats;
+  a.ws = static_cast<char *>(workspace);
+  a.split_bytes = split_bytes;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
   // Column slices per output row: enough that a merge thread folds at most

@@ -105,9 +105,9 @@ def workspace_programs(table_width: int, pages_per_block: int, layout: PageLayou
 
 
 def split_state_bytes(q_len: int, layout: PageLayout) -> int:
-    """Bytes of one split's state: per KV head and live row, m, l and D fp32 accumulators."""
+    """Bytes of one split's state: per KV head and live row, D fp16 outputs, then fp32 m and l."""
     rows = int(q_len) * GQA
-    return layout.hkv * rows * (layout.head_dim + 2) * 4
+    return layout.hkv * rows * (2 * layout.head_dim + 8)
 
 
 def attn_workspace_bytes(max_splits: int, q_len: int, layout: PageLayout) -> int:

@@ -90,8 +90,8 @@ def test_workspace_bytes_rejects_bad_shapes(lib):
     assert lib.k8v4_attn_workspace_bytes(0, 32, 1, 1, 4, 128, 0) == -1
     assert lib.k8v4_attn_workspace_bytes(1, 32, 1, 1, 3, 128, 0) == -1
     assert lib.k8v4_attn_workspace_bytes(1, 32, 1, 1, 4, 96, 0) == -1
-    # An explicit split count fixes the size: splits x hkv x q_len x 6 x (D + 2) x 4 bytes.
-    assert lib.k8v4_attn_workspace_bytes(4, 2048, 1, 7, 4, 128, 64) == 64 * 4 * 7 * 6 * 130 * 4
+    # An explicit split count fixes the size: splits x hkv x q_len x 6 x (2 D + 8) bytes.
+    assert lib.k8v4_attn_workspace_bytes(4, 2048, 1, 7, 4, 128, 64) == 64 * 4 * 7 * 6 * (2 * 128 + 8)
 
 
 def test_ops_layer_raises_without_gpu_tensors(lib):
