@@ -627,19 +627,26 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
 
 template <int D, int NT, int HKV, int NWH>
 struct SplitConfig {
-  // Two waves per head keep the int8 Q operands in LDS (shared by the pair);
-  // one wave per head keeps Q in registers.  Each wave owns a K ring of RK
-  // slots and a V ring of RV slots, the K ring as deep as the LDS allows;
-  // with two waves per SIMD a K slot is refilled as soon as its QK^T product
-  // is issued, so while a wave computes one chunk up to RK - 1 K slots and
-  // RV - 1 V slots are in flight.
-  static constexpr bool QLDS = NWH > 1;
+  // The int8 Q operands live in LDS with two waves per head (shared by the
+  // pair) and with one wave per head at D = 256 when a two-slot K ring still
+  // fits beside them (held in registers they would be spilled: the 256-dim
+  // output accumulators take most of them); otherwise in registers.  Each
+  // wave owns a K ring of RK slots and a V ring of RV slots, the K ring as
+  // deep as the LDS allows; with two waves per SIMD a K slot is refilled as
+  // soon as its QK^T product is issued, so while a wave computes one chunk
+  // up to RK - 1 K slots and RV - 1 V slots are in flight.
   static constexpr int WAVES = HKV * NWH;
   static constexpr int Q_FRAG_BYTES = NT * (D / 64) * kWave * 16;         // int8 B-operand fragments
-  static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_FRAG_BYTES + NT * 16 * 4 : 0;  // + per-row factors
-  static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
+  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4;         // + per-row factors
   // 4 / HKV work-groups share a CU (the grid is about that many per CU).
   static constexpr int LDS_MAX = 163840 * HKV / 4;
+  static constexpr bool QLDS =
+      NWH > 1 || (D == 256 && HKV * Q_LDS_BYTES + WAVES * (2 * Slot<D>::K_BYTES + 2 * Slot<D>::V_BYTES) <= LDS_MAX);
+  // Raw query rows reach LDS-resident fragments through a DMA staging area
+  // in the K ring (two waves per head) or through registers (one wave).
+  static constexpr bool QSTAGE_LDS = NWH > 1;
+  static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_LDS_BYTES : 0;
+  static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
   // One wave per SIMD (NWH == 1) has no partner wave to cover the table
   // lookup of a mid-chunk refill: it refills its K slot after P.V, next to
   // the V slot.
@@ -660,7 +667,7 @@ struct SplitConfig {
   static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
   // The query rows of a wave's tiles are staged in its K slots 1..RK-1.
-  static_assert(!QLDS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
+  static_assert(!QSTAGE_LDS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
                 "query staging does not fit the K ring");
 };
 
@@ -700,9 +707,9 @@ void decode_split_kernel(DecodeArgs a) {
   // loaded here, before the ring's first loads, so they do not wait behind
   // them (vector loads complete in order); with Q in LDS they are staged by
   // direct-to-LDS loads further down.
-  uint4 qraw[CFG::QLDS ? 1 : NT][KS][2];
+  uint4 qraw[CFG::QSTAGE_LDS ? 1 : NT][KS][2];
 #pragma unroll
-  for (int nt = 0; nt < (CFG::QLDS ? 0 : NT); ++nt) {
+  for (int nt = 0; nt < (CFG::QSTAGE_LDS ? 0 : NT); ++nt) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = make_uint4(0u, 0u, 0u, 0u);
     const int r = 16 * nt + n;
@@ -777,7 +784,7 @@ void decode_split_kernel(DecodeArgs a) {
   // a plain count of this wave's own loads.  Rows past the last query row
   // load row 0 and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if constexpr (CFG::QLDS) {
+  if constexpr (CFG::QSTAGE_LDS) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -798,7 +805,7 @@ void decode_split_kernel(DecodeArgs a) {
   }
   const int q_done = issued;
   fill_slot(0);
-  if constexpr (CFG::QLDS) wait_vm(issued - q_done);
+  if constexpr (CFG::QSTAGE_LDS) wait_vm(issued - q_done);
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
@@ -814,7 +821,7 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         uint4 w0, w1;
-        if constexpr (CFG::QLDS) {
+        if constexpr (CFG::QSTAGE_LDS) {
           const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
           const bool live = 16 * nt + n < rows;
           const v4i r0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row);
