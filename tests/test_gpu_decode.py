@@ -257,6 +257,34 @@ def test_zero_length_rows_and_output_dtypes(gpu_ops):
     assert_close(outbf.float().cpu().numpy(), want_bf, atol=8e-3, rtol=2e-2, what="bf16 out")
 
 
+def test_values_near_the_fp16_limit_survive_the_split_states(gpu_ops):
+    """Every 7th token's V row alternates 60000 / -65504, whose -65504 codes
+    dequantize beyond the fp16 range (-8 * 125504 / 15 = -66935), and its K row draws
+    almost all of the softmax weight: the outputs exceed 65504 in magnitude.
+    The split states (fp16, a quarter of each split's normalized output) and
+    their merge must stay finite and match the oracle for fp32 output."""
+    lay = PageLayout(4, 128)
+    cache = Cache(64, lay)
+    gen = torch.Generator().manual_seed(41)
+    table = random_tables(gen, [3000], 64)
+    L = 3000
+    t = torch.arange(L)
+    slots = (table[0].long()[t // PAGE] * PAGE + t % PAGE).to(DEV)
+    k = seeded_normal(gen, (L, 4, 128))
+    v = seeded_normal(gen, (L, 4, 128))
+    k[::7] = 4.0
+    v[::7, :, 0::2] = 60000.0
+    v[::7, :, 1::2] = -65504.0
+    cache.store(gpu_ops, k.to(DEV), v.to(DEV), slots)
+    q = seeded_normal(gen, (3, 24, 128)).abs()
+    seq = torch.tensor([L])
+    want = _oracle(cache, q, table, seq, 3)
+    assert np.abs(want).max() > 65504.0
+    for splits in (0, 23):
+        out = decode(gpu_ops, cache, q, table, seq, 3, out_dtype=torch.float32, num_splits=splits)
+        assert_close(out.cpu().numpy(), want, what="large V, %d splits" % splits)
+
+
 def test_split_count_does_not_change_the_answer(gpu_ops):
     lay = PageLayout(4, 128)
     cache = Cache(300, lay)
