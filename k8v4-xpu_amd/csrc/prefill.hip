@@ -16,9 +16,10 @@
 //    buffer of a two-buffer MFMA tile ring.  Each page is a 64-key tile shared
 //    by all waves (all GQA rows) of the group.
 //  * Dequantization is split so the per-element work is shared by the whole
-//    work-group and exact: K codes become fp16 integers (byte permute into the
-//    mantissa of 1024.0, then subtract 1152), the K scale is applied to the
-//    score column; V nibbles become fp16 subnormals (n * 2^-24 for even dims,
+//    work-group: K codes become fp16 integers (byte permute into the mantissa
+//    of 1024.0, then subtract 1152) times the token's K scale and the
+//    exp2-domain softmax factor (one fp16 rounding, as a bf16/fp16 dequant
+//    has); V nibbles become exact fp16 subnormals (n * 2^-24 for even dims,
 //    16 n * 2^-24 for odd dims) in a transposed tile, the V scale multiplies
 //    P and the zero point is subtracted once per row at the end:
 //      sum_t p_t (n_t - z_t) s_t = sum_t (p_t s_t) n_t - sum_t (p_t s_t) z_t.
@@ -187,11 +188,18 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
     if (c >= T::KCHUNKS) break;
     const int key = c / (D / 16), part = c % (D / 16);
     const uint4 w = *reinterpret_cast<const uint4 *>(stage + 16 * c);
+    // K scale times the exp2-domain softmax factor, folded into the tile (a
+    // key past the sequence gets 0: its unwritten plane may hold anything).
+    const float ks = reinterpret_cast<const float *>(buf + T::S_OFF)[key];
+    const float kc = p * 64 + key < a.seq_len ? ks * a.c : 0.f;
+    const v2h kc2 = {static_cast<_Float16>(kc), static_cast<_Float16>(kc)};
     v2h h[8];
     k_codes_to_f16(w.x, h[0], h[1]);
     k_codes_to_f16(w.y, h[2], h[3]);
     k_codes_to_f16(w.z, h[4], h[5]);
     k_codes_to_f16(w.w, h[6], h[7]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] *= kc2;
     char *row = buf + key * T::KROW;
     const uint4 c0 = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
                                 __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
@@ -230,7 +238,6 @@ __device__ __forceinline__ void convert_page(const PrefillArgs &a, int p, const 
     // Keys past the sequence may hold anything (unwritten planes): zero them
     // so a masked probability never meets a NaN scale.
     const bool live = p * 64 + tid < a.seq_len;
-    s[tid] = live ? s[tid] * a.c : 0.f;
     s[64 + tid] = live ? s[64 + tid] : 0.f;
     s[128 + tid] = live ? s[128 + tid] : 0.f;
   }
@@ -381,18 +388,10 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
         S[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], S[mt], 0, 0, 0);
       }
 
-    // ---- scaled scores, masks, lazy max
+    // ---- scores (already scaled: the K tile carries k_scale * c), masks, lazy max
     const float *sc = reinterpret_cast<const float *>(buf + T::S_OFF);
     const bool masked = p >= full_pages;
     float mx = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4f ksc = *reinterpret_cast<const v4f *>(sc + 32 * mt + 8 * j + 4 * hh);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) S[mt][4 * j + i] *= ksc[i];
-      }
     // The causal mask touches only the last pages of a block: a uniform
     // branch, so the common pages carry no per-score compare and select.
     if (__builtin_expect(masked, 0)) {
