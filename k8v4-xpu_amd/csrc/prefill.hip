@@ -375,11 +375,13 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
     const bool more = p + 1 < p_hi;
     if (more) stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + (bi ^ 1) * T::BUF + T::S_OFF));
 
-    // ---- S^T = K Q^T for the 64 keys of page p: lane (r, hh) reg 4j+i of
-    // tile mt holds key 32*mt + 8*j + 4*hh + i of row r.
-    // The two 32-key tiles alternate, so consecutive MFMAs never wait on
-    // each other's accumulator.
-    v16f S[2] = {(v16f)0.f, (v16f)0.f};
+    // ---- S^T = K Q^T - m for the 64 keys of page p: lane (r, hh) reg 4j+i
+    // of tile mt holds key 32*mt + 8*j + 4*hh + i of row r.  The accumulators
+    // start at -m (the row's running max, 0 before the first visible key), so
+    // the exp2 argument needs no subtraction.  The two 32-key tiles
+    // alternate, so consecutive MFMAs never wait on each other's accumulator.
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    v16f S[2] = {(v16f)(-m_use), (v16f)(-m_use)};
 #pragma unroll
     for (int ds = 0; ds < T::DS; ++ds)
 #pragma unroll
@@ -388,7 +390,8 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
         S[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], S[mt], 0, 0, 0);
       }
 
-    // ---- scores (already scaled: the K tile carries k_scale * c), masks, lazy max
+    // ---- scores (already scaled: the K tile carries k_scale * c, and offset
+    // by -m_use), masks, lazy max
     const float *sc = reinterpret_cast<const float *>(buf + T::S_OFF);
     const bool masked = p >= full_pages;
     float mx = -INFINITY;
@@ -407,24 +410,30 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, S[mt][e]);
-    {
+    // A row's max passes the threshold exactly when one of its two lanes'
+    // does, so the cross-lane max is only taken on a rescale.  Before the
+    // first visible key (m = -inf) any finite score moves the max.
+    const float thr = m_run == -INFINITY ? -INFINITY : kThreshold;
+    if (__ballot(mx > thr)) {
       auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    if (__ballot(mx > m_run + kThreshold)) {
-      const float mnew = fmaxf(m_run, mx);
+      const float rmx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) + m_use;
+      const float mnew = fmaxf(m_run, rmx);
       const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew);
       m_run = mnew;
       lsum *= alpha;
       corr *= alpha;
 #pragma unroll
       for (int dt = 0; dt < T::DT; ++dt) O[dt] *= alpha;
+      // Move the scores to the new max (a row still without a visible key
+      // keeps m = -inf and offset 0).
+      const float delta = m_run == -INFINITY ? 0.f : m_run - m_use;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) S[mt] -= delta;
     }
 
     // ---- P' = exp2(x - m) * v_scale as the fp16 B operand; row sums and zero-point terms.
     // A row with no visible key yet (a segment that starts inside the causal
     // tail) keeps m = -inf; its masked scores then give p = 0.
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     v8h pb[4];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -435,7 +444,7 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
         const v4f vzc = *reinterpret_cast<const v4f *>(sc + 128 + kb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(S[mt][4 * j + i] - m_use);
+          const float pr = __builtin_amdgcn_exp2f(S[mt][4 * j + i]);
           lsum += pr;
           const float pv = pr * vsc[i];
           corr = fmaf(pv, vzc[i], corr);
