@@ -46,10 +46,14 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Lazy-rescale threshold (log2 units): a probability stays <= 2^4 before the
-// running max is moved.  P is multiplied by the token's V scale in fp16, and
-// 16 * scale stays finite for any V row whose range fits fp16.
+// Lazy-rescale threshold (log2 units): the running max m moves only when a
+// score passes it by more than 4, so exp2(score - m) <= 16.  P is carried as
+// exp2(score - m - 2), a quarter of the probability (row sums and outputs
+// shrink alike, so their ratio is unchanged), and is multiplied by the
+// token's V scale in fp16: a V row spanning the whole fp16 range has scale
+// 2 * 65504 / 15, and 16 / 4 * 2 * 65504 / 15 = 34,936 stays finite.
 constexpr float kRescaleThreshold = 4.0f;
+constexpr float kPLog2Offset = 2.0f;
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -550,7 +554,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
   v8h PA[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const float nm = -fmaxf(st.m_run[nt], -FLT_MAX);
+    const float nm = -fmaxf(st.m_run[nt], -FLT_MAX) - kPLog2Offset;
     float p[8];
 #pragma unroll
     for (int ml = 0; ml < 2; ++ml)

@@ -28,7 +28,7 @@
 //    is the MFMA column, so a lane pair owns one row's softmax state and the
 //    score tile is already the B operand of the PV product.
 //  * Online softmax in the exp2 domain with a lazy rescale (the running max
-//    only moves when a row's max grows by more than 2^8).
+//    only moves when a row's max grows by more than 2^2).
 #include "k8v4_common.h"
 
 #include <algorithm>
@@ -42,7 +42,10 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
-constexpr float kThreshold = 8.0f;
+// Lazy-rescale threshold (log2 units): p stays <= 2^2 before a row's running
+// max moves, so P' = p * v_scale stays a finite fp16 even for a V row spanning
+// the whole fp16 range (4 * 2 * 65504 / 15 = 34,936).
+constexpr float kThreshold = 2.0f;
 constexpr uint32_t kEvenNib = 0x000F000Fu;
 constexpr uint32_t kOddNib = 0x00F000F0u;
 
