@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package may import this
 package; only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` use it, and only as the checker or the timed CPU baseline.
+leg of ``bench.py`` use it, and only as the reference results a kernel is
+compared with or as the timed CPU baseline.
 
 It restates, independently of the product code, the reference's rules:
 
