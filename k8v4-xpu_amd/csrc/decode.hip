@@ -858,8 +858,11 @@ void decode_split_kernel(DecodeArgs a) {
         for (int e = 0; e < 16; ++e) {
           // float64 as the reference: |q| = floor(|x| * inv + 0.5) (the
           // reference's ceil(y - 0.5) for y < 0 is the same magnitude).
+          // |x| <= amax keeps |x| * inv within 1e-13 of 127 at most, so the
+          // reference's clamp to 127 never acts, and the truncating
+          // conversion of the positive ay + 0.5 is its floor.
           const double ay = static_cast<double>(fabsf(x[ks][e])) * inv;
-          const int32_t qa = static_cast<int32_t>(fmin(floor(ay + 0.5), 127.0));
+          const int32_t qa = static_cast<int32_t>(ay + 0.5);
           const int32_t qi = x[ks][e] < 0.f ? -qa : qa;
           wq[e >> 2] |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * (e & 3));
         }
