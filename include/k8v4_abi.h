@@ -130,8 +130,9 @@ int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
  *      kernel pages e*pages_per_block .. +pages_per_block-1).
  * Query row j is token seq_len - q_len + j and attends to keys
  * t <= seq_len - q_len + j (bottom-right causal); K and V are the cache's
- * codes dequantized exactly as dequant.py:96-106; softmax(scale * q.k),
- * fp32 accumulation.
+ * codes dequantized as dequant.py:96-106 (K as code * k_scale rounded once
+ * to fp16 on the MFMA tile, V exact); softmax(scale * q.k), fp32
+ * accumulation.
  * out: [q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride
  *      (multiple of 4, base 16-byte aligned).
  * workspace: caller-owned device scratch (16-byte aligned) of workspace_bytes
