@@ -94,6 +94,22 @@ def test_workspace_bytes_rejects_bad_shapes(lib):
     assert lib.k8v4_attn_workspace_bytes(4, 2048, 1, 7, 4, 128, 64) == 64 * 4 * 7 * 6 * (2 * 128 + 8)
 
 
+@pytest.mark.parametrize("hkv,d,q_len,splits", [(4, 128, 7, 64), (2, 256, 7, 512), (4, 128, 1, 3),
+                                                 (2, 128, 10, 17), (4, 256, 4, 256)])
+def test_workspace_bytes_match_the_python_sizing(lib, hkv, d, q_len, splits):
+    """The host-side sizing (plan.attn_workspace_bytes, used by the backend's
+    scratch) and the library agree for an explicit split count."""
+    from k8v4_v030.layout import PageLayout
+    from k8v4_v030.plan import attn_workspace_bytes, split_state_bytes
+
+    lay = PageLayout(hkv, d)
+    got = lib.k8v4_attn_workspace_bytes(1, 4096, 1, q_len, hkv, d, splits)
+    assert got == attn_workspace_bytes(splits, q_len, lay) == splits * split_state_bytes(q_len, lay)
+    assert split_state_bytes(q_len, lay) % 16 == 0  # every split state starts 16-byte aligned
+    # The grid never has fewer splits than sequences.
+    assert lib.k8v4_attn_workspace_bytes(8, 4096, 1, q_len, hkv, d, 3) == attn_workspace_bytes(8, q_len, lay)
+
+
 def test_ops_layer_raises_without_gpu_tensors(lib):
     import torch
 
