@@ -237,6 +237,31 @@ def test_batch_of_eight_matches_per_sequence(gpu_ops):
     assert_close(batched.float().cpu().numpy(), _oracle(cache, qcat, bt, torch.tensor(lens), q_len), what="batch8")
 
 
+@pytest.mark.parametrize("num_splits", [0, 70, 101])
+def test_batch_beyond_one_wave(gpu_ops, num_splits):
+    """70 ragged sequences (some empty): the split plan and the merge walk the
+    lengths 64 at a time; default grid, one split per sequence (grid = batch)
+    and an odd grid."""
+    print("batch 70, splits %d" % num_splits, flush=True)
+    lay = PageLayout(2, 128)
+    q_len = 2
+    gen = torch.Generator().manual_seed(70 + num_splits)
+    lengths = torch.randint(q_len, 3000, (70,), generator=gen)
+    lengths[[5, 33, 64, 69]] = 0
+    pages = [(int(L) + 63) // 64 for L in lengths]
+    cache = Cache(sum(pages) + 1, lay)
+    bt = torch.zeros((70, max(pages)), dtype=torch.int32)
+    off = 0
+    for b, L in enumerate(lengths.tolist()):
+        bt[b, : pages[b]] = torch.arange(off, off + pages[b], dtype=torch.int32)
+        off += pages[b]
+        if L:
+            fill_sequence(gpu_ops, cache, gen, bt[b], L)
+    q = seeded_normal(gen, (70 * q_len, 12, 128))
+    out = decode(gpu_ops, cache, q, bt, lengths, q_len, out_dtype=torch.float32, num_splits=num_splits)
+    assert_close(out.cpu().numpy(), _oracle(cache, q, bt, lengths, q_len), what="batch 70")
+
+
 def test_zero_length_rows_and_output_dtypes(gpu_ops):
     lay = PageLayout(4, 128)
     cache = Cache(8, lay)
