@@ -262,6 +262,25 @@ def test_batch_beyond_one_wave(gpu_ops, num_splits):
     assert_close(out.cpu().numpy(), _oracle(cache, q, bt, lengths, q_len), what="batch 70")
 
 
+def test_explicit_visible_ends_out_of_order(gpu_ops):
+    """visible_lens rows [max_end, end_0 .. end_{q-1}] that are not the causal
+    staircase (tree-verify style: ends out of order, down to a single key)."""
+    lay = PageLayout(4, 128)
+    q_len = 5
+    lens = [5000, 2300]
+    vis_rows = [[4999, 4990, 3000, 4999, 1, 2500], [2300, 64, 2300, 1777, 65, 2]]
+    gen = torch.Generator().manual_seed(5005)
+    table = random_tables(gen, lens, 130)
+    cache = Cache(130, lay)
+    for b, L in enumerate(lens):
+        fill_sequence(gpu_ops, cache, gen, table[b], L)
+    q = seeded_normal(gen, (2 * q_len, 24, 128))
+    seq = torch.tensor(lens)
+    vis = torch.tensor(vis_rows, dtype=torch.int32)
+    out = decode(gpu_ops, cache, q, table, seq, q_len, visible=vis, out_dtype=torch.float32)
+    assert_close(out.cpu().numpy(), _oracle(cache, q, table, seq, q_len, visible=vis), what="explicit ends")
+
+
 def test_zero_length_rows_and_output_dtypes(gpu_ops):
     lay = PageLayout(4, 128)
     cache = Cache(8, lay)
