@@ -26,7 +26,8 @@ def _oracle(cache, q, table, seq_lens, q_len, ppb=1, visible=None):
 
 
 @pytest.mark.parametrize("hkv,d,q_len", [(4, 128, 7), (4, 128, 1), (2, 128, 3), (4, 128, 10),
-                                         (2, 256, 7), (4, 256, 1), (2, 256, 2)])
+                                         (2, 256, 7), (4, 256, 1), (2, 256, 2), (4, 256, 5), (2, 256, 9),
+                                         (4, 256, 10)])
 def test_decode_matches_oracle_small(gpu_ops, hkv, d, q_len):
     print("decode small hkv=%d d=%d q=%d" % (hkv, d, q_len), flush=True)
     lay = PageLayout(hkv, d)
