@@ -13,8 +13,10 @@ non-contiguous block tables.  Prints ONE JSON line:
   the stream it runs on (the library records one between its two kernels),
   against the 8 TB/s HBM peak; ``traffic`` comes from the committed
   rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
-* ``cpu_baseline``: the float64 oracle (oracle/attention.py) over the whole
-  headline step, single-threaded, on this host;
+* ``cpu_baseline``: the reference's PyTorch path restated in torch
+  (oracle/torch_cpu.py) on every host core: the whole headline decode step,
+  config 2's store and a sample of config 5's prefill; the float64 oracle
+  checks the GPU's headline output;
 * ``step_graph_us`` and the configs' ``graph_us_*``: per-launch time from HIP
   graphs of back-to-back launches replayed between two events (median and
   min of several replays), which leaves out the host launch cost;
@@ -30,6 +32,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -353,49 +356,121 @@ def traffic_from_profile():
 
 
 # --------------------------------------------------------------------- CPU baseline
-def cpu_baseline(torch, work, min_seconds=10.0, max_reps=5):
-    """The float64 oracle on the whole headline step (all sequences), one thread.
+def host_cpu():
+    """(logical cores, CPU model name) of this host."""
+    model = "unknown"
+    try:
+        import subprocess
 
-    Repeats the step until ``min_seconds`` of CPU work (at most ``max_reps``)
-    and reports the median repetition; also returns the largest deviation of
-    the GPU output from the oracle on the same cache."""
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except Exception:  # noqa: BLE001 -- the model name is informational
+        pass
+    return os.cpu_count() or 1, model
+
+
+def median_seconds(fn, reps=3, warmup=1):
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline(torch, work, store_work=None, prefill_work=None):
+    """The reference's PyTorch path (oracle/torch_cpu.py) on every host core.
+
+    decode: the whole headline step (4 x 131,072 tokens, q = 7) -- gather and
+    dequantize, int8 query rows, fp32 attention; store: config 2's 16,896 tokens
+    quantized into the cache; prefill: the last rows of config 5's chunk over all
+    135,296 keys (key-tiled online softmax).  Median of 3 after one warm-up.
+    The float64 oracle checks the GPU's headline output on the same cache."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
 
-    from oracle import attention, paged
+    from oracle import attention, paged, torch_cpu
 
-    work.launch(0)  # copy 0, whose table the oracle reads
+    cores, model = host_cpu()
+    torch.set_num_threads(cores)
+    work.launch(0)  # copy 0, whose tables the CPU reads
     torch.cuda.synchronize()
     geom = paged.Geometry(work.hkv, work.head_dim)
     raw_pages = work.raw.view(work.num_pages, work.layout.page_bytes)
-    seqs = []
+    # The sequences' pages, gathered into one compact host cache with an identity-like table.
+    tables = []
+    blobs = []
+    base = 0
     for b, n in enumerate(work.lengths):
         pages = -(-n // PAGE)
-        table = work.tables[0][b, :pages].long()
-        blob = raw_pages.index_select(0, table).view(torch.uint8).cpu().numpy().reshape(-1)
+        blobs.append(raw_pages.index_select(0, work.tables[0][b, :pages].long()).view(torch.uint8).cpu())
+        tables.append(torch.arange(base, base + pages, dtype=torch.int64))
+        base += pages
+    raw = torch.cat([x.reshape(-1) for x in blobs])
+    views = torch_cpu.region_views(raw, geom)
+    table = torch.nn.utils.rnn.pad_sequence(tables, batch_first=True)
+    q = work.q.cpu()
+    sec = median_seconds(lambda: torch_cpu.decode(views, q, table, work.lengths, work.q_len))
+    gpu = work.out.double().cpu().numpy()
+    blob = raw.numpy()
+    err = 0.0
+    for b, n in enumerate(work.lengths):
         rows = slice(b * work.q_len, (b + 1) * work.q_len)
-        seqs.append((n, pages, blob, work.q[rows].cpu().numpy(), work.out[rows].double().cpu().numpy()))
-    reps, err = [], 0.0
-    with threadpool_limits(1):
-        while len(reps) < max_reps and (len(reps) < 1 or sum(reps) < min_seconds):
-            t0 = time.perf_counter()
-            outs = [attention.decode_attention(q, blob, geom, np.arange(pages)[None], [n], work.q_len)
-                    for n, pages, blob, q, _ in seqs]
-            reps.append(time.perf_counter() - t0)
-            err = max(float(np.abs(seqs[i][4] - outs[i]).max()) for i in range(len(seqs)))
-    sec = sorted(reps)[len(reps) // 2]
-    return {
-        "value": round(work.kv_bytes / sec / 1e9, 4),
+        want = attention.decode_attention(q[rows].numpy(), blob, geom, table[b : b + 1].numpy(), [n], work.q_len)
+        err = max(err, float(np.abs(gpu[rows] - want).max()))
+    out = {
+        "value": round(work.kv_bytes / sec / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": cores,
+        "cpu_model": model,
         "kind": "port",
-        "sample": "float64 numpy oracle (oracle/attention.py decode_attention) over the whole headline "
-                  "step: %d sequences x %d cached tokens, %d query tokens, 24 Q / 4 KV heads, D=128 "
-                  "(%d KV bytes); median of %d repetitions, 1 BLAS thread"
-                  % (work.batch, work.lengths[0], work.q_len, work.kv_bytes, len(reps)),
+        "sample": "the whole headline step on the host: torch restatement of the reference's CPU path "
+                  "(oracle/torch_cpu.py decode: gather + dequantize %d x %d tokens, int8 query rows, fp32 "
+                  "attention over 24 Q / 4 KV heads, D=128); median of 3 after 1 warm-up, %d threads"
+                  % (work.batch, work.lengths[0], cores),
         "seconds": round(sec, 3),
-        "gpu_vs_oracle_max_abs_err": err,
+        "us_per_layer": round(sec * 1e6, 1),
+        "gpu_vs_float64_oracle_max_abs_err": err,
     }
+    if store_work is not None:
+        out["store"] = cpu_store_baseline(torch, store_work, torch_cpu, geom)
+    if prefill_work is not None:
+        out["prefill"] = cpu_prefill_baseline(torch, prefill_work, torch_cpu)
+    return out
+
+
+def cpu_store_baseline(torch, w, torch_cpu, geom):
+    """Config 2 on the host: quantize 4 x 4,224 tokens into a 16,384-page cache."""
+    call = w.inputs[0]
+    k, v, slots = (t.cpu() for t in call._keep[:3])
+    raw = torch.zeros(w.num_pages * w.layout.page_bytes, dtype=torch.uint8)
+    views = torch_cpu.region_views(raw, geom)
+    sec = median_seconds(lambda: torch_cpu.store(views, k, v, slots))
+    return {"value": round(w.algo_bytes / sec / 1e9, 3), "unit": "GB/s", "us_per_layer": round(sec * 1e6, 1),
+            "sample": "config 2 whole: %d tokens x 4 KV heads quantized (float64 rule) into the paged cache"
+                      % w.ntok}
+
+
+def cpu_prefill_baseline(torch, w, torch_cpu, rows=512):
+    """The last ``rows`` query tokens of config 5's chunk over all its keys, on the host."""
+    from oracle import paged
+
+    geom = paged.Geometry(w.layout.hkv, w.layout.head_dim)
+    raw = w.raw.view(torch.uint8).cpu()
+    views = torch_cpu.region_views(raw, geom)
+    q = w.q[-rows:].cpu()
+    row = w.row.cpu()
+    sec = median_seconds(lambda: torch_cpu.prefill(views, q, row, w.seq_len, 1.0 / math.sqrt(w.layout.head_dim)))
+    pairs = rows * (w.seq_len - rows) + rows * (rows + 1) // 2
+    flops = pairs * 6 * w.layout.hkv * 4 * w.layout.head_dim
+    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "seconds": round(sec, 3),
+            "full_chunk_us_estimate": round(sec * w.flops / flops * 1e6, 0),
+            "sample": "last %d of the %d query tokens over all %d keys (key tiles of 16,384, row groups of 256, "
+                      "fp32)" % (rows, w.q_len, w.seq_len)}
 
 
 # --------------------------------------------------------------------- configs
@@ -548,8 +623,11 @@ def main(argv=None) -> int:
         },
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(torch, work)
-        progress("cpu baseline: %.1f s" % line["cpu_baseline"]["seconds"])
+        store_w = StoreWorkload(o, torch, copies=1, seed=1002)
+        prefill_w = PrefillWorkload(o, torch)
+        line["cpu_baseline"] = cpu_baseline(torch, work, store_w, prefill_w)
+        progress("cpu baseline: decode %.1f s" % line["cpu_baseline"]["seconds"])
+        del store_w, prefill_w
     del work
     torch.cuda.empty_cache()
     if not args.no_configs:

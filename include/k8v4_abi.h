@@ -40,6 +40,12 @@ enum {
 
 enum { K8V4_F16 = 0, K8V4_BF16 = 1, K8V4_F32 = 2 };
 
+/* Query layouts of k8v4_q_quant. */
+enum {
+  K8V4_Q_TOKENS = 0, /* token rows [ntok, 6*hkv, head_dim], token stride q_tok_stride */
+  K8V4_Q_PADDED = 1  /* the padded tile [hkv, 64, head_dim] itself */
+};
+
 int k8v4_abi_version(void);
 
 /* Message of this thread's last failed call ("" if none). */
@@ -62,6 +68,32 @@ int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype, int64_t k_t
                         float *v_scale, float *v_zero, int64_t num_pages, int64_t k_page_stride,
                         int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
                         int64_t vz_page_stride, void *stream);
+
+/*
+ * K-only and V-only quantize-and-write (replace torch.ops.xe2_kv.k_store_paged
+ * and v_store_paged, k8v4_v030/native/xe2_kv_ops.cpp:1371-1409): the K half or
+ * the V half of k8v4_kv_store_paged, same rules, same skipped slots.
+ */
+int k8v4_k_store_paged(const void *k, int src_dtype, int64_t k_tok_stride, const int64_t *slot_mapping,
+                       int64_t ntok, int hkv, int head_dim, int8_t *k_cache, float *k_scale, int64_t num_pages,
+                       int64_t k_page_stride, int64_t ks_page_stride, void *stream);
+int k8v4_v_store_paged(const void *v, int src_dtype, int64_t v_tok_stride, const int64_t *slot_mapping,
+                       int64_t ntok, int hkv, int head_dim, uint8_t *v_cache, float *v_scale, float *v_zero,
+                       int64_t num_pages, int64_t v_page_stride, int64_t vs_page_stride, int64_t vz_page_stride,
+                       void *stream);
+
+/*
+ * Query quantization into the int8 Q-once tile (replaces torch.ops.xe2_kv.q_quant_once
+ * and the pack-and-quantize step of int8k_int4v_s1_varlen_from_q,
+ * k8v4_v030/native/xe2_kv_ops.cpp:205-294, :1248-1265, :1670-1690).
+ * q8: int8 [hkv][64][head_dim]; q_scale: fp32 [hkv][64].  Row r of head h is
+ * query token r / 6 of query head h*6 + r % 6 (K8V4_Q_TOKENS, ntok*6 <= 64;
+ * rows from ntok*6 on get zero codes and scale) or row r of the padded input
+ * (K8V4_Q_PADDED).  Codes follow the K rule of k8v4_v030/oracle.py:22-40 in
+ * float64, the rule the decode kernels apply to fp16/bf16 queries.
+ */
+int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_tok_stride, int64_t ntok, int hkv,
+                 int head_dim, int8_t *q8, float *q_scale, void *stream);
 
 /*
  * Paged decode / MTP verify for a batch with one common query length
@@ -94,6 +126,23 @@ int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8
                     const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
                     int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
                     void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
+
+/*
+ * k8v4_attn_batch over pre-quantized queries (replaces torch.ops.xe2_kv.
+ * int8k_int4v_s1_paged and int8k_int4v_s1_varlen_paged, k8v4_v030/native/
+ * xe2_kv_ops.cpp:1628-1660, which take the Q-once tile k8v4_q_quant writes).
+ * q8 / q_scale: per sequence one tile as k8v4_q_quant writes it, sequences
+ * q8_seq_stride / qs_seq_stride elements apart (q8 16-byte aligned, stride a
+ * multiple of 16).  Every other argument as k8v4_attn_batch.
+ */
+int k8v4_attn_batch_q8(const int8_t *q8, const float *q_scale, int64_t q8_seq_stride, int64_t qs_seq_stride,
+                       const int8_t *k_cache, const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                       const float *v_zero, int64_t num_pages, int64_t k_page_stride, int64_t ks_page_stride,
+                       int64_t v_page_stride, int64_t vs_page_stride, int64_t vz_page_stride,
+                       const int32_t *block_table, int64_t bt_stride, int64_t table_width, int pages_per_block,
+                       const int32_t *seq_lens, const int32_t *visible_lens, int64_t vis_stride, int64_t batch,
+                       int q_len, int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                       void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
 
 /*
  * k8v4_attn_batch for timing its two kernels apart.  `split_done_event`

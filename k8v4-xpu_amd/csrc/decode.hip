@@ -59,6 +59,12 @@ struct DecodeArgs {
   const uint16_t *q;
   int64_t q_tok_stride;  // elements; head stride is head_dim
   int q_bf16;
+  // Pre-quantized query instead of q (nullable): per sequence an int8 tile
+  // [hkv][64][head_dim] (row r of head h is token r / 6, query head
+  // h * 6 + r % 6) and fp32 scales [hkv][64], the reference's Q-once layout.
+  const int8_t *q8;
+  const float *q8_scale;
+  int64_t q8_seq_stride, qs_seq_stride;  // elements between sequences
   const int8_t *k_cache;
   const float *k_scale;
   const uint8_t *v_cache;
@@ -280,10 +286,15 @@ __device__ __forceinline__ int kswz(int t) {
 // 16-token halves of the transposed QK^T output tile.
 __device__ __forceinline__ int chunk_token(int g, int i) { return i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4); }
 
-// Direct-to-LDS loads.  K and V are read exactly once, so they carry the
-// nontemporal policy (streaming reads measured ~15% faster on MI355X); the
-// scale planes, shared by the heads of a work-group, and the query rows,
-// shared by the splits of a sequence, use the default policy.
+// Direct-to-LDS loads.  K rows (one 128-byte line per token and head) are
+// read exactly once and carry the nontemporal policy (streaming reads
+// measured faster on MI355X).  A V row is half of a 128-byte line whose other
+// half is the neighbouring head's row, read by another wave of the same
+// work-group moments later: with the nontemporal policy that line was often
+// fetched twice (HBM reads 1.08x the algorithmic bytes), with the default
+// policy once (1.005x) at the same speed.  The scale planes, shared by the
+// heads of a work-group, and the query rows, shared by the splits of a
+// sequence, also use the default policy.
 constexpr int kPolicyNontemporal = 2;
 
 __device__ __forceinline__ void dma16_nt(const void *src, lds_t *dst) {
@@ -360,7 +371,7 @@ __device__ __forceinline__ void issue_v(const DecodeArgs &a, const int32_t *bt_r
                    static_cast<int64_t>(tok0) * HKV * S::VROW;
 #pragma unroll
   for (int j = 0; j < S::NV; ++j)
-    dma16_nt(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, vslot + j * 1024);
+    dma16(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, vslot + j * 1024);
   const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4 + lo.s;
   const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0;
   const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0;
@@ -707,6 +718,10 @@ void decode_split_kernel(DecodeArgs a) {
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
 
+  // A pre-quantized query tile (k8v4_attn_batch_q8) replaces the raw rows
+  // and their quantization below.
+  const bool pre_q = a.q8 != nullptr;  // uniform over the launch
+
   // Raw query words.  With Q in registers (one wave per head) they are
   // loaded here, before the ring's first loads, so they do not wait behind
   // them (vector loads complete in order); with Q in LDS they are staged by
@@ -717,7 +732,7 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = make_uint4(0u, 0u, 0u, 0u);
     const int r = 16 * nt + n;
-    if (r < rows) {
+    if (r < rows && !pre_q) {
       const int j = r / kGqa;
       const int qh = h * kGqa + (r - j * kGqa);
       const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
@@ -788,7 +803,7 @@ void decode_split_kernel(DecodeArgs a) {
   // a plain count of this wave's own loads.  Rows past the last query row
   // load row 0 and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if constexpr (CFG::QSTAGE_LDS) {
+  if (CFG::QSTAGE_LDS && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -813,8 +828,37 @@ void decode_split_kernel(DecodeArgs a) {
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
-  // both waves of the head quantize (they need crow) and wave 0 stores.
-  {
+  // each wave quantizes its own tiles (nt % NWH == w) and publishes them.
+  if (pre_q) {
+    // The tile's codes already are the B operands: lane (n, g) of tile nt
+    // takes row 16 nt + n, dims 64 ks + 16 g .. + 15; dead rows stay zero.
+    const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(h) * kPage * D;
+    const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + h * kPage;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if constexpr (CFG::QLDS) {
+        if (nt % NWH != w) continue;
+      }
+      const int r = 16 * nt + n;
+      const bool live = r < rows;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v4i frag = live ? *reinterpret_cast<const v4i *>(tile + static_cast<int64_t>(r) * D + 64 * ks + 16 * g)
+                              : (v4i){0, 0, 0, 0};
+        if constexpr (CFG::QLDS) {
+          *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16) = frag;
+        } else {
+          st.qb[nt][ks] = frag;
+        }
+      }
+      const double c = static_cast<double>(live ? scales[r] : 0.f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
+      st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+      if constexpr (CFG::QLDS) {
+        if (g == 0)
+          reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
+      }
+    }
+  } else {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -855,17 +899,8 @@ void decode_split_kernel(DecodeArgs a) {
       for (int ks = 0; ks < KS; ++ks) {
         uint32_t wq[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          // float64 as the reference: |q| = floor(|x| * inv + 0.5) (the
-          // reference's ceil(y - 0.5) for y < 0 is the same magnitude).
-          // |x| <= amax keeps |x| * inv within 1e-13 of 127 at most, so the
-          // reference's clamp to 127 never acts, and the truncating
-          // conversion of the positive ay + 0.5 is its floor.
-          const double ay = static_cast<double>(fabsf(x[ks][e])) * inv;
-          const int32_t qa = static_cast<int32_t>(ay + 0.5);
-          const int32_t qi = x[ks][e] < 0.f ? -qa : qa;
-          wq[e >> 2] |= (static_cast<uint32_t>(qi) & 0xFFu) << (8 * (e & 3));
-        }
+        for (int e = 0; e < 16; ++e)
+          wq[e >> 2] |= (static_cast<uint32_t>(k_rule_code(x[ks][e], inv)) & 0xFFu) << (8 * (e & 3));
         const v4i frag = (v4i){static_cast<int>(wq[0]), static_cast<int>(wq[1]), static_cast<int>(wq[2]),
                                static_cast<int>(wq[3])};
         if constexpr (CFG::QLDS) {
@@ -1214,7 +1249,8 @@ extern "C" int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width,
 namespace k8v4 {
 namespace {
 
-int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache, const float *k_scale,
+int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q8, const float *q8_scale,
+               int64_t q8_seq_stride, int64_t qs_seq_stride, const int8_t *k_cache, const float *k_scale,
                const uint8_t *v_cache, const float *v_scale, const float *v_zero, int64_t num_pages,
                int64_t k_page_stride, int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
                int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride, int64_t table_width,
@@ -1231,15 +1267,24 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
   K8V4_REQUIRE(num_pages >= 1, "empty cache");
   K8V4_REQUIRE(batch >= 1 && batch < (1 << 24), "empty batch");
   K8V4_REQUIRE(table_width >= 1 && table_width * pages_per_block < (int64_t(1) << 30), "block_table width");
-  K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
+  if (q8) {
+    K8V4_REQUIRE(q8_scale, "null pointer");
+    K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q8) % 16 == 0 && q8_seq_stride % 16 == 0 &&
+                     q8_seq_stride >= int64_t(hkv) * kPage * head_dim && qs_seq_stride >= int64_t(hkv) * kPage,
+                 "q8 must be 16-byte aligned [batch][hkv][64][head_dim] tiles with [batch][hkv][64] scales");
+  } else {
+    K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
+  }
   K8V4_REQUIRE(out_dtype == K8V4_F16 || out_dtype == K8V4_BF16 || out_dtype == K8V4_F32,
                "out dtype must be fp16, bf16 or fp32");
-  K8V4_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && v_zero && block_table && seq_lens && out &&
-                   workspace,
+  K8V4_REQUIRE((q || q8) && k_cache && k_scale && v_cache && v_scale && v_zero && block_table && seq_lens &&
+                   out && workspace,
                "null pointer");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
-               "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
-  K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+  if (!q8) {
+    K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
+                 "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
+    K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+  }
   K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim, "out token stride shorter than HQ*D");
   K8V4_REQUIRE(bt_stride >= table_width, "block_table row stride shorter than its width");
   K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && k_page_stride % 16 == 0,
@@ -1267,6 +1312,10 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k
   a.q = static_cast<const uint16_t *>(q);
   a.q_tok_stride = q_tok_stride;
   a.q_bf16 = q_dtype == K8V4_BF16;
+  a.q8 = q8;
+  a.q8_scale = q8_scale;
+  a.q8_seq_stride = q8_seq_stride;
+  a.qs_seq_stride = qs_seq_stride;
   a.k_cache = k_cache;
   a.k_scale = k_scale;
   a.v_cache = v_cache;
@@ -1347,11 +1396,33 @@ extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride,
                                const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
                                int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
                                void *workspace, int64_t workspace_bytes, int num_splits, void *stream) {
-  return k8v4::attn_batch(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
-                          k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
-                          block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
-                          vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
-                          workspace_bytes, num_splits, stream, nullptr, 3);
+  return k8v4::attn_batch(q, q_dtype, q_tok_stride, nullptr, nullptr, 0, 0, k_cache, k_scale, v_cache, v_scale,
+                          v_zero, num_pages, k_page_stride, ks_page_stride, v_page_stride, vs_page_stride,
+                          vz_page_stride, block_table, bt_stride, table_width, pages_per_block, seq_lens,
+                          visible_lens, vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride,
+                          workspace, workspace_bytes, num_splits, stream, nullptr, 3);
+}
+
+extern "C" int k8v4_attn_batch_q8(const int8_t *q8, const float *q_scale, int64_t q8_seq_stride,
+                                  int64_t qs_seq_stride, const int8_t *k_cache, const float *k_scale,
+                                  const uint8_t *v_cache, const float *v_scale, const float *v_zero,
+                                  int64_t num_pages, int64_t k_page_stride, int64_t ks_page_stride,
+                                  int64_t v_page_stride, int64_t vs_page_stride, int64_t vz_page_stride,
+                                  const int32_t *block_table, int64_t bt_stride, int64_t table_width,
+                                  int pages_per_block, const int32_t *seq_lens, const int32_t *visible_lens,
+                                  int64_t vis_stride, int64_t batch, int q_len, int hkv, int head_dim, void *out,
+                                  int out_dtype, int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
+                                  int num_splits, void *stream) {
+  if (!q8) {
+    k8v4::clear_error();
+    k8v4::set_error("null pointer");
+    return K8V4_ERR_ARG;
+  }
+  return k8v4::attn_batch(nullptr, K8V4_F16, 0, q8, q_scale, q8_seq_stride, qs_seq_stride, k_cache, k_scale,
+                          v_cache, v_scale, v_zero, num_pages, k_page_stride, ks_page_stride, v_page_stride,
+                          vs_page_stride, vz_page_stride, block_table, bt_stride, table_width, pages_per_block,
+                          seq_lens, visible_lens, vis_stride, batch, q_len, hkv, head_dim, out, out_dtype,
+                          out_tok_stride, workspace, workspace_bytes, num_splits, stream, nullptr, 3);
 }
 
 extern "C" int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
@@ -1364,10 +1435,10 @@ extern "C" int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_to
                                         int q_len, int hkv, int head_dim, void *out, int out_dtype,
                                         int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
                                         int num_splits, void *stream, void *split_done_event, int stages) {
-  return k8v4::attn_batch(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
-                          k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
-                          block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens,
-                          vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride, workspace,
-                          workspace_bytes, num_splits, stream, static_cast<hipEvent_t>(split_done_event),
+  return k8v4::attn_batch(q, q_dtype, q_tok_stride, nullptr, nullptr, 0, 0, k_cache, k_scale, v_cache, v_scale,
+                          v_zero, num_pages, k_page_stride, ks_page_stride, v_page_stride, vs_page_stride,
+                          vz_page_stride, block_table, bt_stride, table_width, pages_per_block, seq_lens,
+                          visible_lens, vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride,
+                          workspace, workspace_bytes, num_splits, stream, static_cast<hipEvent_t>(split_done_event),
                           stages);
 }

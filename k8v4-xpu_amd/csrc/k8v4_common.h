@@ -43,4 +43,18 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t bits, bool is_bf16)
   return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
 
+// One element's code under the K rule of k8v4_v030/oracle.py:22-40 (also the
+// reference's query rule, oracle.py:145): q = round_half_away(x * inv) with
+// inv = 1 / (amax / 127), all in float64.  |q| = floor(|x| * inv + 0.5); with
+// |x| <= amax the product stays within 1e-13 of 127, so the reference's clamp
+// to 127 never acts and the truncating conversion of the positive |x| * inv +
+// 0.5 is its floor.  The caller passes inv = 0 for an all-zero row.  The
+// multiply and the add round separately (no contraction into an fma).
+__device__ __forceinline__ int32_t k_rule_code(float x, double inv) {
+#pragma clang fp contract(off)
+  const double ay = static_cast<double>(fabsf(x)) * inv;
+  const int32_t qa = static_cast<int32_t>(ay + 0.5);
+  return x < 0.f ? -qa : qa;
+}
+
 }  // namespace k8v4

@@ -40,7 +40,10 @@ struct StoreArgs {
   int hkv;
   int bf16;
   int vec_ok;  // 16-byte aligned rows: one vector load per lane
+  int parts;   // kStoreK | kStoreV: which of K and V this launch writes
 };
+
+constexpr int kStoreK = 1, kStoreV = 2;
 
 // E consecutive fp16/bf16 values -> fp32.
 template <int E>
@@ -97,20 +100,27 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
 
   // The slot first: its load then shares the round trip of the K/V loads.
   const int64_t slot = a.slots[token];
+  const bool do_k = a.parts & kStoreK, do_v = a.parts & kStoreV;  // uniform over the launch
   float kx[E], vx[E];
-  load_row<E>(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, kx);
-  load_row<E>(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, vx);
+  if (do_k) load_row<E>(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, kx);
+  if (do_v) load_row<E>(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, vx);
 
-  float amax = 0.f, lo = vx[0], hi = vx[0];
+  float amax = 0.f, lo = 0.f, hi = 0.f;
+  if (do_k) {
 #pragma unroll
-  for (int i = 0; i < E; ++i) {
-    amax = fmaxf(amax, fabsf(kx[i]));
-    lo = fminf(lo, vx[i]);
-    hi = fmaxf(hi, vx[i]);
+    for (int i = 0; i < E; ++i) amax = fmaxf(amax, fabsf(kx[i]));
+    amax = group_max<LPU>(amax);
   }
-  amax = group_max<LPU>(amax);
-  lo = group_min<LPU>(lo);
-  hi = group_max<LPU>(hi);
+  if (do_v) {
+    lo = hi = vx[0];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      lo = fminf(lo, vx[i]);
+      hi = fmaxf(hi, vx[i]);
+    }
+    lo = group_min<LPU>(lo);
+    hi = group_max<LPU>(hi);
+  }
 
   const int64_t page = slot >= 0 ? slot / kPage : -1;
   if (!live || page < 0 || page >= a.num_pages) return;
@@ -125,6 +135,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   // path, step for step as the rule is written.
   constexpr float kMargin = 0x1p-12f;
 
+  if (do_k) {
   // K: symmetric int8, scale amax/127, round half away from zero.
   const double k_scale = amax == 0.f ? 0.0 : static_cast<double>(amax) / 127.0;
   uint32_t kw[E / 4] = {};
@@ -150,6 +161,15 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
       kw[i >> 2] |= b << (8 * (i & 3));
     }
   }
+  char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + E * sub;
+#pragma unroll
+  for (int c = 0; c < E / 16; ++c)
+    reinterpret_cast<uint4 *>(kdst)[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
+  if (sub == 0)
+    *reinterpret_cast<float *>(reinterpret_cast<char *>(a.k_scale) + page * a.ks_ps + cell * 4) =
+        static_cast<float>(k_scale);
+  }
+  if (!do_v) return;
 
   // V: affine uint4 over the whole row, floor(x + 0.5) rounding.
   const double lo_d = lo, hi_d = hi;
@@ -170,15 +190,9 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     vw[i >> 3] |= static_cast<uint32_t>(q) << (4 * (i & 7));
   }
 
-  char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + E * sub;
-#pragma unroll
-  for (int c = 0; c < E / 16; ++c)
-    reinterpret_cast<uint4 *>(kdst)[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
   char *vdst = reinterpret_cast<char *>(a.v_cache) + page * a.v_ps + cell * (D / 2) + (E / 2) * sub;
   *reinterpret_cast<uint2 *>(vdst) = make_uint2(vw[0], vw[1]);
   if (sub == 0) {
-    *reinterpret_cast<float *>(reinterpret_cast<char *>(a.k_scale) + page * a.ks_ps + cell * 4) =
-        static_cast<float>(k_scale);
     *reinterpret_cast<float *>(reinterpret_cast<char *>(a.v_scale) + page * a.vs_ps + cell * 4) =
         static_cast<float>(v_scale);
     *reinterpret_cast<float *>(reinterpret_cast<char *>(a.v_zero) + page * a.vz_ps + cell * 4) =
@@ -191,16 +205,18 @@ bool aligned(const void *p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p
 }  // namespace
 }  // namespace k8v4
 
-extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
-                                   int64_t k_tok_stride, int64_t v_tok_stride,
-                                   const int64_t *slot_mapping, int64_t ntok, int hkv,
-                                   int head_dim, int8_t *k_cache, float *k_scale,
-                                   uint8_t *v_cache, float *v_scale, float *v_zero,
-                                   int64_t num_pages, int64_t k_page_stride,
-                                   int64_t ks_page_stride, int64_t v_page_stride,
-                                   int64_t vs_page_stride, int64_t vz_page_stride, void *stream) {
-  using namespace k8v4;
+
+namespace k8v4 {
+namespace {
+
+// The three store entry points: parts selects K, V or both.
+int store_paged(int parts, const void *k, const void *v, int src_dtype, int64_t k_tok_stride, int64_t v_tok_stride,
+                const int64_t *slot_mapping, int64_t ntok, int hkv, int head_dim, int8_t *k_cache, float *k_scale,
+                uint8_t *v_cache, float *v_scale, float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride, int64_t vz_page_stride,
+                void *stream, const char *what) {
   clear_error();
+  const bool do_k = parts & kStoreK, do_v = parts & kStoreV;
   K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)",
                hkv);
   K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)",
@@ -208,18 +224,18 @@ extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
   K8V4_REQUIRE(src_dtype == K8V4_F16 || src_dtype == K8V4_BF16, "k/v dtype must be fp16 or bf16");
   K8V4_REQUIRE(ntok >= 0 && num_pages >= 0, "negative token or page count");
   if (ntok == 0) return K8V4_OK;
-  K8V4_REQUIRE(k && v && slot_mapping && k_cache && k_scale && v_cache && v_scale && v_zero,
+  K8V4_REQUIRE(slot_mapping && (!do_k || (k && k_cache && k_scale)) && (!do_v || (v && v_cache && v_scale && v_zero)),
                "null pointer");
-  K8V4_REQUIRE(k_tok_stride >= static_cast<int64_t>(hkv) * head_dim &&
-                   v_tok_stride >= static_cast<int64_t>(hkv) * head_dim,
+  K8V4_REQUIRE((!do_k || k_tok_stride >= static_cast<int64_t>(hkv) * head_dim) &&
+                   (!do_v || v_tok_stride >= static_cast<int64_t>(hkv) * head_dim),
                "k/v token stride shorter than hkv*head_dim");
-  K8V4_REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 8) && aligned(k_scale, 4) &&
-                   aligned(v_scale, 4) && aligned(v_zero, 4) && aligned(slot_mapping, 8),
+  K8V4_REQUIRE(aligned(slot_mapping, 8) && (!do_k || (aligned(k_cache, 16) && aligned(k_scale, 4))) &&
+                   (!do_v || (aligned(v_cache, 8) && aligned(v_scale, 4) && aligned(v_zero, 4))),
                "cache region or slot pointer misaligned");
-  K8V4_REQUIRE(k_page_stride % 16 == 0 && v_page_stride % 8 == 0 && ks_page_stride % 4 == 0 &&
-                   vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
+  K8V4_REQUIRE((!do_k || (k_page_stride % 16 == 0 && ks_page_stride % 4 == 0)) &&
+                   (!do_v || (v_page_stride % 8 == 0 && vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0)),
                "cache page strides must keep rows aligned");
-  K8V4_REQUIRE(aligned(k, 2) && aligned(v, 2), "k/v pointers misaligned");
+  K8V4_REQUIRE((!do_k || aligned(k, 2)) && (!do_v || aligned(v, 2)), "k/v pointers misaligned");
 
   StoreArgs a;
   a.k = static_cast<const uint16_t *>(k);
@@ -241,7 +257,8 @@ extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
   a.vz_ps = vz_page_stride;
   a.hkv = hkv;
   a.bf16 = src_dtype == K8V4_BF16;
-  a.vec_ok = aligned(k, 16) && aligned(v, 16) && (k_tok_stride % 8 == 0) && (v_tok_stride % 8 == 0);
+  a.vec_ok = (!do_k || (aligned(k, 16) && k_tok_stride % 8 == 0)) && (!do_v || (aligned(v, 16) && v_tok_stride % 8 == 0));
+  a.parts = parts;
 
   const int upw = kWave / (head_dim / 16);
   const int64_t waves = (a.units + upw - 1) / upw;
@@ -252,5 +269,39 @@ extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
     kv_store_kernel<128><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(a);
   else
     kv_store_kernel<256><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(a);
-  return launch_status("k8v4_kv_store_paged");
+  return launch_status(what);
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int k8v4_kv_store_paged(const void *k, const void *v, int src_dtype,
+                                   int64_t k_tok_stride, int64_t v_tok_stride,
+                                   const int64_t *slot_mapping, int64_t ntok, int hkv,
+                                   int head_dim, int8_t *k_cache, float *k_scale,
+                                   uint8_t *v_cache, float *v_scale, float *v_zero,
+                                   int64_t num_pages, int64_t k_page_stride,
+                                   int64_t ks_page_stride, int64_t v_page_stride,
+                                   int64_t vs_page_stride, int64_t vz_page_stride, void *stream) {
+  return k8v4::store_paged(k8v4::kStoreK | k8v4::kStoreV, k, v, src_dtype, k_tok_stride, v_tok_stride,
+                           slot_mapping, ntok, hkv, head_dim, k_cache, k_scale, v_cache, v_scale, v_zero,
+                           num_pages, k_page_stride, ks_page_stride, v_page_stride, vs_page_stride,
+                           vz_page_stride, stream, "k8v4_kv_store_paged");
+}
+
+extern "C" int k8v4_k_store_paged(const void *k, int src_dtype, int64_t k_tok_stride, const int64_t *slot_mapping,
+                                  int64_t ntok, int hkv, int head_dim, int8_t *k_cache, float *k_scale,
+                                  int64_t num_pages, int64_t k_page_stride, int64_t ks_page_stride, void *stream) {
+  return k8v4::store_paged(k8v4::kStoreK, k, nullptr, src_dtype, k_tok_stride, 0, slot_mapping, ntok, hkv,
+                           head_dim, k_cache, k_scale, nullptr, nullptr, nullptr, num_pages, k_page_stride,
+                           ks_page_stride, 0, 0, 0, stream, "k8v4_k_store_paged");
+}
+
+extern "C" int k8v4_v_store_paged(const void *v, int src_dtype, int64_t v_tok_stride, const int64_t *slot_mapping,
+                                  int64_t ntok, int hkv, int head_dim, uint8_t *v_cache, float *v_scale,
+                                  float *v_zero, int64_t num_pages, int64_t v_page_stride, int64_t vs_page_stride,
+                                  int64_t vz_page_stride, void *stream) {
+  return k8v4::store_paged(k8v4::kStoreV, nullptr, v, src_dtype, 0, v_tok_stride, slot_mapping, ntok, hkv,
+                           head_dim, nullptr, nullptr, v_cache, v_scale, v_zero, num_pages, 0, 0, v_page_stride,
+                           vs_page_stride, vz_page_stride, stream, "k8v4_v_store_paged");
 }

@@ -34,8 +34,8 @@ COMMON_FLAGS = [
 # The store reproduces float64 rounding step for step: no fused multiply-adds.
 # The decode kernels never produce or consume NaN (unwritten tails are masked
 # by selection before any arithmetic), so max/min need no NaN quieting.
-PER_FILE_FLAGS = {"kv_store.hip": ["-ffp-contract=off"], "decode.hip": ["-fno-honor-nans"],
-                  "prefill.hip": ["-fno-honor-nans"]}
+PER_FILE_FLAGS = {"kv_store.hip": ["-ffp-contract=off"], "q_quant.hip": ["-ffp-contract=off"],
+                  "decode.hip": ["-fno-honor-nans"], "prefill.hip": ["-fno-honor-nans"]}
 
 
 def hipcc() -> str:

@@ -1,28 +1,28 @@
 """vLLM attention backend for the K8/V4 cache on MI355X (2 or 4 local KV heads).
 
-The caller of the hot path: vLLM owns the block table and the slot map, this
-module turns its per-step metadata into the three library entry points.
-Reference: k8v4_v030/backend.py:1-486 (vLLM 0.30 XPU backend) -- same class
-names, metadata fields, checks and error messages, so a vLLM that selects the
-reference backend can select this one (``AttentionBackendEnum.CUSTOM``).
+This is the caller of the hot path: vLLM owns the block table and the slot
+map; the backend turns one engine step's metadata into the library's three
+entry points (quantize-and-write, batched decode / MTP verify, chunked
+prefill).  The vLLM-facing surface follows the reference backend
+(k8v4_v030/backend.py:56-486): the class names, the metadata fields, the
+constructor and forward signatures, the capture support and the error
+messages callers and tests match.  The implementation is this package's own:
 
-What differs on MI355X:
-  * no staging copies: the store takes vLLM's fp16/bf16 ``key``/``value``
-    rows and the decode op its ``query`` and ``output`` rows in place (the
-    library takes token strides and bf16), where the reference first copies
-    them into fp16 scratch buffers (backend.py:342-343, :416-418);
-  * prefill runs on the HIP chunked-prefill kernel (``hip_prefill``) instead
-    of the eager gather / oneDNN paths (backend.py:376-409);
-  * stream capture is ``torch.cuda.is_current_stream_capturing`` (HIP graphs);
-    decode is capturable, prefill is refused inside a graph, as in the
-    reference;
-  * the reference's W4A8 MLP hook and its per-stage timing/profiling wrappers
-    are not part of the attention path and are not carried over.
+* the metadata builder turns ``query_start_loc`` into a step plan once per
+  step (decode runs of equal query length, and the prefill sequences), which
+  every layer's ``forward`` then walks;
+* vLLM's fp16/bf16 ``query`` / ``key`` / ``value`` / ``output`` rows go to
+  the kernels in place (they take token strides and bf16), so there are no
+  staging copies;
+* decode runs use the scratch's decode workspace and prefill sequences its
+  prefill workspace, both allocated before capture (``scratch.py``), so no
+  call allocates;
+* a step made only of decode runs of one query length is one launch pair and
+  can be captured in a HIP graph; a step with prefill refuses capture.
 """
-
 from __future__ import annotations
 
-from dataclasses import replace
+from dataclasses import dataclass, replace
 
 import torch
 
@@ -43,47 +43,60 @@ from vllm.v1.kv_cache_interface import AttentionSpec
 from .cache_views import bind_regions
 from .layout import CACHE_DTYPE, DECODE_MAX_T, PAGE, PageLayout, attention_pages_per_block
 from .ops_api import ops
-from .plan import (
-    layout_for_heads,
-    query_segments,
-    require_decoder,
-    scratch_capacity,
-    token_span,
-    uniform_packed_q_len,
-    workspace_programs,
-)
-from .prefill import hip_prefill
-from .scratch import ensure_scratch, get_scratch, scratch_ready
+from .plan import layout_for_heads, query_segments, require_decoder, scratch_capacity, token_span, uniform_packed_q_len
+from .scratch import Scratch, ensure_scratch, get_scratch, scratch_ready
 
 logger = init_logger(__name__)
 
-
-def _require_page_ratio(cache: torch.Tensor, pages_per_block: int, layout: PageLayout) -> None:
-    """The block-table entry must cover the cache block the slot map uses.
-
-    The live layer is ``[block, head, token, slot_bytes]`` (slot_bytes = 1.5 D
-    + 12).  ``token // 64`` is the kernel-page count of one entry; a 2112-token
-    entry is 33 pages and is passed through as ``pages_per_block``.
-    (backend.py:59-79)
-    """
-    slot = layout.slot_bytes_per_head
-    if cache.ndim != 4 or int(cache.shape[-1]) != slot:
-        raise RuntimeError(
-            "K8/V4 cache shape %s is not [block, head, token, %d]" % (tuple(cache.shape), slot)
-        )
-    tokens = int(cache.shape[-2])
-    if tokens % PAGE != 0:
-        raise RuntimeError("K8/V4 block has %d tokens, not a multiple of %d" % (tokens, PAGE))
-    ratio = tokens // PAGE
-    if ratio != int(pages_per_block):
-        raise RuntimeError(
-            "K8/V4 pages_per_block %s does not match the %d-token cache block (%d pages)"
-            % (pages_per_block, tokens, ratio)
-        )
+_REGIONS = ("k", "k_scale", "v", "v_scale", "v_zero")
 
 
+# --------------------------------------------------------------- step plan
+@dataclass(frozen=True)
+class DecodeRun:
+    """Requests ``first .. first + count - 1``, each with ``q_len`` query tokens
+    packed from token ``tok0``: one batched decode launch."""
+
+    first: int
+    count: int
+    q_len: int
+    tok0: int
+
+
+@dataclass(frozen=True)
+class PrefillSeq:
+    """Request ``req``'s ``width`` query tokens from token ``tok0``: one prefill launch."""
+
+    req: int
+    tok0: int
+    width: int
+
+
+def plan_step(query_starts: tuple[int, ...]) -> tuple[tuple[DecodeRun, ...], tuple[PrefillSeq, ...]]:
+    """Split a step into decode runs (1..10 query tokens) and prefill sequences (longer)."""
+    runs: list[DecodeRun] = []
+    seqs: list[PrefillSeq] = []
+    for first, count, q_len in query_segments(query_starts):
+        if q_len == 0:
+            continue
+        if q_len <= DECODE_MAX_T:
+            tok0, _ = token_span(query_starts, first, count, q_len)
+            runs.append(DecodeRun(first, count, q_len, tok0))
+        else:
+            for req in range(first, first + count):
+                tok0, width = token_span(query_starts, req, 1, q_len)
+                seqs.append(PrefillSeq(req, tok0, width))
+    return tuple(runs), tuple(seqs)
+
+
+def attention_pages(manager_block: int, kernel_block: int | None) -> int:
+    """Kernel pages per block-table entry (layout.attention_pages_per_block)."""
+    return attention_pages_per_block(int(manager_block), kernel_block)
+
+
+# ---------------------------------------------------------------- metadata
 class Xe2K8V4Metadata(AttentionMetadata):
-    """Per-step attention metadata (backend.py:82-110)."""
+    """One step's attention metadata (fields of backend.py:82-110) plus its plan."""
 
     def __init__(
         self,
@@ -100,72 +113,53 @@ class Xe2K8V4Metadata(AttentionMetadata):
         packed_q_len: int,
         layout: PageLayout,
     ):
-        self.seq_lens = seq_lens
-        self.slot_mapping = slot_mapping
-        self.block_table = block_table
-        self.query_start_loc = query_start_loc
-        self.query_starts = query_starts
-        self.seq_lens_cpu = seq_lens_cpu
-        self.num_actual_tokens = num_actual_tokens
-        self.max_query_len = max_query_len
-        self.max_seq_len = max_seq_len
-        self.pages_per_block = pages_per_block
-        self.packed_q_len = packed_q_len
-        self.layout = layout
-
-
-def attention_pages(manager_block: int, kernel_block: int | None) -> int:
-    return attention_pages_per_block(int(manager_block), kernel_block)
+        for name, value in list(locals().items()):
+            if name != "self":
+                setattr(self, name, value)
+        self.decode_runs, self.prefill_seqs = plan_step(tuple(query_starts))
 
 
 class Xe2K8V4MetadataBuilder(AttentionMetadataBuilder[Xe2K8V4Metadata]):
-    """Builds ``Xe2K8V4Metadata`` and sizes the per-device scratch (backend.py:113-185).
+    """Per-step metadata and the device scratch, sized from the engine config.
 
-    A uniform batch (every request the same query length, at most 10 tokens)
-    is one decode launch and can be captured in a graph.
+    A uniform batch (every request 1..10 query tokens, the same count) is one
+    decode launch and may be captured; MTP verify steps join the decode group.
     """
 
     _cudagraph_support = AttentionCGSupport.UNIFORM_BATCH
 
     def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
         super().__init__(kv_cache_spec, layer_names, vllm_config, device)
-        head = int(getattr(kv_cache_spec, "head_size", 256))
-        self.layout = PageLayout(int(kv_cache_spec.num_kv_heads), head)
+        self.layout = PageLayout(int(kv_cache_spec.num_kv_heads), int(getattr(kv_cache_spec, "head_size", 256)))
         logger.info_once("K8/V4 local heads: %d KV / %d Q", self.layout.hkv, self.layout.hq)
-        # MTP with a q = 7 verify step joins the decode group.
         self._init_reorder_batch_threshold(1, supports_spec_as_decode=True)
+
+    def _pages_per_entry(self) -> int:
+        return attention_pages(self.kv_cache_spec.block_size, getattr(self, "kernel_block_size", None))
 
     def set_kernel_block_size(self, kernel_block_size: int) -> None:
         super().set_kernel_block_size(kernel_block_size)
-        manager = int(self.kv_cache_spec.block_size)
-        ratio = attention_pages(manager, self.kernel_block_size)
         logger.info_once(
             "K8/V4 pages per block-table entry: %d (manager block %d, kernel block %s)",
-            ratio,
-            manager,
+            self._pages_per_entry(),
+            int(self.kv_cache_spec.block_size),
             self.kernel_block_size,
         )
         self._ensure_scratch()
 
-    def _ensure_scratch(self) -> None:
-        spec = self.kv_cache_spec
-        manager = int(spec.block_size)
-        model = self.vllm_config.model_config
-        sched = self.vllm_config.scheduler_config
-        comp = getattr(self.vllm_config, "compilation_config", None)
-        capture = []
-        if comp is not None:
-            capture = list(getattr(comp, "cudagraph_capture_sizes", None) or [])
-        nprog, store_tokens, out_tokens = scratch_capacity(
-            int(model.max_model_len),
-            manager,
+    def _ensure_scratch(self) -> Scratch:
+        cfg = self.vllm_config
+        capture = getattr(getattr(cfg, "compilation_config", None), "cudagraph_capture_sizes", None) or []
+        capacity = scratch_capacity(
+            int(cfg.model_config.max_model_len),
+            int(self.kv_cache_spec.block_size),
             getattr(self, "kernel_block_size", None),
-            int(sched.max_num_batched_tokens),
-            int(sched.max_num_seqs),
-            capture,
+            int(cfg.scheduler_config.max_num_batched_tokens),
+            int(cfg.scheduler_config.max_num_seqs),
+            list(capture),
             self.layout,
         )
-        ensure_scratch(self.device, self.layout, nprog, store_tokens, out_tokens)
+        return ensure_scratch(self.device, self.layout, *capacity)
 
     def build(
         self,
@@ -188,14 +182,15 @@ class Xe2K8V4MetadataBuilder(AttentionMetadataBuilder[Xe2K8V4Metadata]):
             num_actual_tokens=int(cam.num_actual_tokens),
             max_query_len=int(cam.max_query_len),
             max_seq_len=int(cam.max_seq_len),
-            pages_per_block=attention_pages(self.kv_cache_spec.block_size, getattr(self, "kernel_block_size", None)),
+            pages_per_block=self._pages_per_entry(),
             packed_q_len=uniform_packed_q_len(starts),
             layout=self.layout,
         )
 
 
+# --------------------------------------------------------------- the layer
 class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
-    """Store and attention for one layer (backend.py:192-431)."""
+    """Quantize-and-write and attention of one layer."""
 
     def __init__(
         self,
@@ -211,25 +206,20 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
         kv_sharing_target_layer_name: str | None = None,
         sinks: torch.Tensor | None = None,
     ) -> None:
-        # A draft model may pass sinks=; a real sink bias is not implemented
-        # and must not be dropped silently (backend.py:207-214).
+        # A sink bias is not implemented; refusing it beats dropping it.
         if sinks is not None:
-            raise RuntimeError(
-                "Xe2K8V4Impl: attention sink bias (sinks) is not implemented on the k8v4 backend"
-            )
+            raise RuntimeError("Xe2K8V4Impl: attention sink bias (sinks) is not implemented on the k8v4 backend")
         if kv_cache_dtype != CACHE_DTYPE:
             raise RuntimeError("K8/V4 impl got kv dtype %s" % kv_cache_dtype)
-        if num_kv_heads is None:
-            num_kv_heads = num_heads
-        self.layout = layout_for_heads(num_heads, num_kv_heads, head_size)
+        kv_heads = num_heads if num_kv_heads is None else num_kv_heads
+        self.layout = layout_for_heads(num_heads, kv_heads, head_size)
         require_decoder(attn_type, sliding_window, alibi_slopes, logits_soft_cap, scale, int(head_size))
-        self.num_heads = num_heads
-        self.num_kv_heads = num_kv_heads
-        self.head_size = head_size
+        self.num_heads, self.num_kv_heads, self.head_size = num_heads, kv_heads, head_size
         self.scale = float(scale)
         self.kv_cache_dtype = kv_cache_dtype
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
 
+    # -- store ---------------------------------------------------------------
     def do_kv_cache_update(
         self,
         layer: torch.nn.Module,
@@ -239,7 +229,7 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
         slot_mapping: torch.Tensor,
     ) -> None:
         del layer
-        cache = _one_cache(kv_cache)
+        cache = _cache_tensor(kv_cache)
         if cache.numel() == 0:
             return
         if slot_mapping.ndim != 1:
@@ -248,14 +238,16 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
         if ntok == 0:
             return
         if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous():
-            raise RuntimeError(
-                "slot_mapping must be contiguous int64, got %s stride %s"
-                % (slot_mapping.dtype, tuple(slot_mapping.stride()))
-            )
-        if key.shape[0] < ntok or value.shape[0] < ntok:
+            raise RuntimeError("slot_mapping must be contiguous int64, got %s stride %s"
+                               % (slot_mapping.dtype, tuple(slot_mapping.stride())))
+        if min(int(key.shape[0]), int(value.shape[0])) < ntok:
             raise RuntimeError("key/value shorter than slot_mapping")
-        _store_kv(key, value, cache, slot_mapping, ntok, self.layout)
+        regions = _regions(cache, self.layout)
+        k = _rows(key[:ntok], self.layout.hkv, self.layout.head_dim, "key")
+        v = _rows(value[:ntok], self.layout.hkv, self.layout.head_dim, "value")
+        ops().kv_store_paged(k, v, slot_mapping, *regions)
 
+    # -- attention -----------------------------------------------------------
     def forward(
         self,
         layer: torch.nn.Module,
@@ -271,170 +263,115 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
         del layer, key, value
         if output_scale is not None or output_block_scale is not None:
             raise RuntimeError("K8/V4 does not take an output scale")
-        cache = _one_cache(kv_cache)
+        cache = _cache_tensor(kv_cache)
         if cache.numel() == 0 or query.shape[0] == 0:
             return output
-        # The builder reads the KV cache spec, the impl reads the attention
-        # module; a mismatch would otherwise surface as a scratch error.
-        if attn_metadata.layout != self.layout:
+        meta = attn_metadata
+        if meta.layout != self.layout:  # builder (cache spec) and impl (module) disagree
             raise RuntimeError(
-                "K8/V4 KV cache was built for %d KV / %d Q heads but the "
-                "attention impl derived %d KV / %d Q"
-                % (attn_metadata.layout.hkv, attn_metadata.layout.hq, self.layout.hkv, self.layout.hq)
-            )
-        q3 = _heads_view(query, self.layout, "query")
-        o3 = _heads_view(output, self.layout, "output")
-        if attn_metadata.packed_q_len:
-            self._packed(q3, cache, attn_metadata, o3)
-            return output
-        if _capturing():
+                "K8/V4 KV cache was built for %d KV / %d Q heads but the attention impl derived %d KV / %d Q"
+                % (meta.layout.hkv, meta.layout.hq, self.layout.hkv, self.layout.hq))
+        _check_block_geometry(cache, meta.pages_per_block, self.layout)
+        lay = self.layout
+        q = _rows(query, lay.hq, lay.head_dim, "query")
+        out = _rows(output, lay.hq, lay.head_dim, "output")
+        regions = _regions(cache, lay)
+        scratch = get_scratch(query.device, lay)
+        if meta.packed_q_len:
+            runs = meta.decode_runs
+            if meta.prefill_seqs or len(runs) != 1 or runs[0].q_len != int(meta.packed_q_len):
+                raise RuntimeError("packed metadata does not match query starts")
+        elif _graph_capturing():
             raise RuntimeError("K8/V4 prefill cannot run inside a HIP graph")
-        self._eager(q3, cache, attn_metadata, o3)
+        for run in meta.decode_runs:
+            self._decode(q, out, regions, meta, run, scratch)
+        if meta.prefill_seqs:
+            lens = meta.seq_lens_cpu if meta.seq_lens_cpu is not None else meta.seq_lens.detach().cpu()
+            for seq in meta.prefill_seqs:
+                self._prefill(q, out, regions, meta, seq, int(lens[seq.req]), scratch)
         return output
 
-    def _packed(self, query: torch.Tensor, cache: torch.Tensor, meta: Xe2K8V4Metadata, output: torch.Tensor) -> None:
-        q_len = int(meta.packed_q_len)
-        if q_len < 1 or q_len > DECODE_MAX_T:
-            raise RuntimeError("packed q_len %d" % q_len)
-        segments = query_segments(meta.query_starts)
-        if len(segments) != 1 or segments[0][2] != q_len:
-            raise RuntimeError("packed metadata does not match query starts")
-        first, count, _ = segments[0]
-        self._attn_batch(query, cache, meta, output, first, count, q_len)
-
-    def _attn_batch(
-        self,
-        query: torch.Tensor,
-        cache: torch.Tensor,
-        meta: Xe2K8V4Metadata,
-        output: torch.Tensor,
-        first: int,
-        count: int,
-        q_len: int,
-    ) -> None:
-        _require_page_ratio(cache, meta.pages_per_block, self.layout)
-        tok0, width = token_span(meta.query_starts, first, count, q_len)
-        if query.shape[0] < tok0 + width:
+    def _decode(self, q, out, regions, meta: Xe2K8V4Metadata, run: DecodeRun, scratch: Scratch) -> None:
+        width = run.count * run.q_len
+        if q.shape[0] < run.tok0 + width:
             raise RuntimeError("query shorter than the packed segment")
-        block_table = meta.block_table
-        if block_table.ndim != 2 or block_table.shape[0] < first + count:
-            raise RuntimeError("block_table shape %s" % (tuple(block_table.shape),))
-        block_table = block_table.narrow(0, first, count)
-        if block_table.dtype != torch.int32 or not block_table.is_contiguous():
-            raise RuntimeError(
-                "block_table must be contiguous int32, got %s stride %s"
-                % (block_table.dtype, tuple(block_table.stride()))
-            )
-        seq_lens = meta.seq_lens
-        if seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous():
-            raise RuntimeError(
-                "seq_lens must be contiguous int32, got %s stride %s" % (seq_lens.dtype, tuple(seq_lens.stride()))
-            )
-        seq_lens = seq_lens.reshape(-1).narrow(0, first, count)
-        scratch = get_scratch(query.device, self.layout)
-        nprog = workspace_programs(int(block_table.shape[1]), meta.pages_per_block, self.layout)
-        partials, m_state, l_state, merged = scratch.workspace(nprog)
-        views = bind_regions(cache, self.layout)
-        # The query and output rows go to the kernel in place: it takes their
-        # token stride and fp16 / bf16 directly.
-        ops().int8k_int4v_attn_batch(
-            query.narrow(0, tok0, width),
-            scratch.q8,
-            scratch.q_scale,
-            views["k"],
-            views["k_scale"],
-            views["v"],
-            views["v_scale"],
-            views["v_zero"],
-            block_table,
-            seq_lens,
-            scratch.visible,
-            partials,
-            m_state,
-            l_state,
-            merged,
-            output.narrow(0, tok0, width),
-            q_len,
-            meta.pages_per_block,
-        )
+        table = meta.block_table
+        if table.ndim != 2 or table.shape[0] < run.first + run.count:
+            raise RuntimeError("block_table shape %s" % (tuple(table.shape),))
+        table = table[run.first : run.first + run.count]
+        if table.dtype != torch.int32 or not table.is_contiguous():
+            raise RuntimeError("block_table must be contiguous int32, got %s stride %s"
+                               % (table.dtype, tuple(table.stride())))
+        lens = meta.seq_lens
+        if lens.dtype != torch.int32 or not lens.is_contiguous():
+            raise RuntimeError("seq_lens must be contiguous int32, got %s stride %s"
+                               % (lens.dtype, tuple(lens.stride())))
+        lens = lens.reshape(-1)[run.first : run.first + run.count]
+        rows = slice(run.tok0, run.tok0 + width)
+        ops().int8k_int4v_attn_batch(q[rows], None, None, *regions, table, lens, None, scratch.decode_ws,
+                                     None, None, None, out[rows], run.q_len, meta.pages_per_block)
 
-    def _eager(self, query: torch.Tensor, cache: torch.Tensor, meta: Xe2K8V4Metadata, output: torch.Tensor) -> None:
-        """A mixed step: uniform decode runs batched, every longer query runs
-        the chunked-prefill kernel on its own sequence (backend.py:376-409)."""
-        views = bind_regions(cache, self.layout)
-        _require_page_ratio(cache, meta.pages_per_block, self.layout)
-        cpu_lens = meta.seq_lens_cpu
-        if cpu_lens is None:
-            cpu_lens = meta.seq_lens.detach().to("cpu")
-        for first, count, q_len in query_segments(meta.query_starts):
-            if q_len == 0:
-                continue
-            if 1 <= q_len <= DECODE_MAX_T:
-                self._attn_batch(query, cache, meta, output, first, count, q_len)
-                continue
-            for offset in range(count):
-                req = first + offset
-                tok0, width = token_span(meta.query_starts, req, 1, q_len)
-                seq_len = int(cpu_lens[req])
-                if seq_len < width:
-                    raise RuntimeError(
-                        "seq_len %d does not cover query %d; the kernel expects "
-                        "the length to include this step" % (seq_len, width)
-                    )
-                row = meta.block_table[req]
-                out_rows = output.narrow(0, tok0, width)
-                q_rows = query.narrow(0, tok0, width)
-                if out_rows.dtype == q_rows.dtype and out_rows.is_contiguous():
-                    hip_prefill(q_rows, views, row, seq_len, meta.pages_per_block, self.scale, out=out_rows)
-                else:
-                    out_rows.copy_(hip_prefill(q_rows, views, row, seq_len, meta.pages_per_block, self.scale))
+    def _prefill(self, q, out, regions, meta: Xe2K8V4Metadata, seq: PrefillSeq, seq_len: int,
+                 scratch: Scratch) -> None:
+        if seq_len < seq.width:
+            raise RuntimeError("seq_len %d does not cover query %d; the kernel expects the length to include "
+                               "this step" % (seq_len, seq.width))
+        row = meta.block_table[seq.req]
+        if row.dtype != torch.int32 or not row.is_contiguous():
+            row = row.to(torch.int32).contiguous()
+        rows = slice(seq.tok0, seq.tok0 + seq.width)
+        ops().prefill_paged(q[rows], *regions, row, seq_len, meta.pages_per_block, self.scale, out[rows],
+                            workspace=scratch.prefill_ws)
 
 
-def _heads_view(x: torch.Tensor, layout: PageLayout, what: str) -> torch.Tensor:
-    """``[T, HQ, D]`` view of vLLM's ``[T, HQ * D]`` or ``[T, HQ, D]`` rows."""
-    if x.dim() == 3:
-        return x
-    if x.dim() == 2 and int(x.shape[1]) == layout.hq * layout.head_dim and x.stride(1) == 1:
-        return x.view(x.shape[0], layout.hq, layout.head_dim) if x.is_contiguous() else x.unflatten(1, (layout.hq, layout.head_dim))
-    raise RuntimeError("%s shape %s is not [T, %d, %d]" % (what, tuple(x.shape), layout.hq, layout.head_dim))
-
-
-def _store_kv(key, value, cache, slot_mapping, ntok: int, layout: PageLayout) -> None:
-    """Quantize-and-write of vLLM's key/value rows in place (no staging copy)."""
-    k = _kv_view(key.narrow(0, 0, ntok), layout, "key")
-    v = _kv_view(value.narrow(0, 0, ntok), layout, "value")
-    views = bind_regions(cache, layout)
-    ops().kv_store_paged(k, v, slot_mapping, views["k"], views["k_scale"], views["v"], views["v_scale"],
-                         views["v_zero"])
-
-
-def _kv_view(x: torch.Tensor, layout: PageLayout, what: str) -> torch.Tensor:
-    if x.dim() == 3:
-        return x
-    if x.dim() == 2 and int(x.shape[1]) == layout.hkv * layout.head_dim and x.stride(1) == 1:
-        return x.unflatten(1, (layout.hkv, layout.head_dim))
-    raise RuntimeError("%s shape %s is not [T, %d, %d]" % (what, tuple(x.shape), layout.hkv, layout.head_dim))
-
-
-def _one_cache(kv_cache: torch.Tensor | list[torch.Tensor] | tuple[torch.Tensor, ...]) -> torch.Tensor:
+# ----------------------------------------------------------------- helpers
+def _cache_tensor(kv_cache) -> torch.Tensor:
+    """The layer's one packed cache tensor (vLLM may hand it over in a list)."""
     if isinstance(kv_cache, (list, tuple)):
         if len(kv_cache) != 1:
             raise RuntimeError("K8/V4 cache is one packed tensor, got %d pieces" % len(kv_cache))
-        return kv_cache[0]
+        kv_cache = kv_cache[0]
     return kv_cache
 
 
-def _capturing() -> bool:
-    cuda = getattr(torch, "cuda", None)
-    fn = getattr(cuda, "is_current_stream_capturing", None)
-    if fn is None or not torch.cuda.is_available():
-        return False
-    return bool(fn())
+def _check_block_geometry(cache: torch.Tensor, pages_per_block: int, layout: PageLayout) -> None:
+    """The cache is ``[block, head, token, slot_bytes]`` and one block is ``pages_per_block`` pages.
+
+    (The reference's page-ratio rule, backend.py:59-79; a 2,112-token manager
+    block is 33 kernel pages and goes to the kernels as such.)"""
+    slot = layout.slot_bytes_per_head
+    if cache.ndim != 4 or int(cache.shape[-1]) != slot:
+        raise RuntimeError("K8/V4 cache shape %s is not [block, head, token, %d]" % (tuple(cache.shape), slot))
+    tokens = int(cache.shape[-2])
+    if tokens % PAGE:
+        raise RuntimeError("K8/V4 block has %d tokens, not a multiple of %d" % (tokens, PAGE))
+    if tokens // PAGE != int(pages_per_block):
+        raise RuntimeError("K8/V4 pages_per_block %s does not match the %d-token cache block (%d pages)"
+                           % (pages_per_block, tokens, tokens // PAGE))
 
 
+def _regions(cache: torch.Tensor, layout: PageLayout) -> tuple[torch.Tensor, ...]:
+    views = bind_regions(cache, layout)
+    return tuple(views[name] for name in _REGIONS)
+
+
+def _rows(x: torch.Tensor, heads: int, head_dim: int, what: str) -> torch.Tensor:
+    """``[T, heads, D]`` view of vLLM's ``[T, heads * D]`` (or already 3-D) rows, no copy."""
+    if x.dim() == 3:
+        return x
+    if x.dim() == 2 and int(x.shape[1]) == heads * head_dim and x.stride(1) == 1:
+        return x.unflatten(1, (heads, head_dim))
+    raise RuntimeError("%s shape %s is not [T, %d, %d]" % (what, tuple(x.shape), heads, head_dim))
+
+
+def _graph_capturing() -> bool:
+    return torch.cuda.is_available() and bool(torch.cuda.is_current_stream_capturing())
+
+
+# ----------------------------------------------------------------- backend
 @register_backend(AttentionBackendEnum.CUSTOM)
 class Xe2K8V4AttentionBackend(AttentionBackend):
-    """The backend class vLLM's selector returns (backend.py:446-486)."""
+    """The class vLLM's selector returns (registered as the CUSTOM backend)."""
 
     accept_output_buffer: bool = True
     forward_includes_kv_cache_update: bool = False
@@ -442,8 +379,8 @@ class Xe2K8V4AttentionBackend(AttentionBackend):
 
     @staticmethod
     def get_name() -> str:
-        # Attention.__init__ does AttentionBackendEnum[get_name()]; CUSTOM is
-        # the registered out-of-tree member.
+        # vLLM looks the name up in AttentionBackendEnum; CUSTOM is the
+        # member registered for out-of-tree backends.
         return AttentionBackendEnum.CUSTOM.name
 
     @staticmethod
@@ -456,7 +393,7 @@ class Xe2K8V4AttentionBackend(AttentionBackend):
 
     @staticmethod
     def get_supported_kernel_block_sizes() -> list[MultipleOf]:
-        return [MultipleOf(64)]
+        return [MultipleOf(PAGE)]
 
     @classmethod
     def get_supported_head_sizes(cls) -> list[int]:
@@ -472,14 +409,17 @@ class Xe2K8V4AttentionBackend(AttentionBackend):
 
     @classmethod
     def customize_spec(cls, spec: AttentionSpec) -> AttentionSpec:
-        head = int(getattr(spec, "head_size", 256))
-        return replace(spec, state_content_bytes=int(head + head // 2 + 12))
+        # One (token, KV head) slot: D int8 K, D/2 packed V, three fp32 planes.
+        return replace(spec, state_content_bytes=PageLayout(4, int(getattr(spec, "head_size", 256))).slot_bytes_per_head)
 
 
 __all__ = [
+    "DecodeRun",
+    "PrefillSeq",
     "Xe2K8V4AttentionBackend",
     "Xe2K8V4Impl",
     "Xe2K8V4Metadata",
     "Xe2K8V4MetadataBuilder",
     "attention_pages",
+    "plan_step",
 ]

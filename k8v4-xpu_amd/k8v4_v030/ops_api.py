@@ -74,6 +74,19 @@ _EXTRA_SYMBOLS.append((
     _i32,
 ))
 _EXTRA_SYMBOLS.append(("k8v4_prefill_workspace_bytes", [_i64, _i64, _i32, _i32], _i64))
+_EXTRA_SYMBOLS.append(("k8v4_k_store_paged", [_vp, _i32, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i64, _vp],
+                       _i32))
+_EXTRA_SYMBOLS.append(("k8v4_v_store_paged",
+                       [_vp, _i32, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _i32))
+_EXTRA_SYMBOLS.append(("k8v4_q_quant", [_vp, _i32, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp], _i32))
+_EXTRA_SYMBOLS.append((
+    "k8v4_attn_batch_q8",
+    [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+     _vp, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _i32,
+     _vp, _i32, _i64, _vp, _i64, _i32, _vp],
+    _i32,
+))
+Q_TOKENS, Q_PADDED = 0, 1
 
 
 def load_library():
@@ -205,6 +218,7 @@ class _Ops:
 
     def __init__(self, lib):
         self._lib = lib
+        self._legacy_ws: dict[torch.device, torch.Tensor] = {}
 
     # -- quantize-and-write ------------------------------------------------
     def kv_store_paged(self, k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero):
@@ -394,11 +408,174 @@ class _Ops:
         ]
         return BoundCall(self._lib, self._lib.k8v4_prefill_paged, args, dev, tensors)
 
-    def k_store_paged(self, *args, **kwargs):
-        raise RuntimeError("k_store_paged: use kv_store_paged (K and V are written by one kernel)")
+    # -- K-only / V-only stores ----------------------------------------------
+    def k_store_paged(self, k_fp16, slot_mapping, k_cache, k_scale):
+        """The K half of :meth:`kv_store_paged` (xe2_kv_ops.cpp:1371-1389)."""
+        _require(k_fp16.dim() == 3 and int(k_fp16.shape[2]) in (128, 256), "k_fp16 [T,HKV,D] with D in (128, 256)")
+        head_dim = int(k_fp16.shape[2])
+        _require(slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous(), "slot_mapping int64")
+        hkv = _checked_hkv(int(k_fp16.shape[1]))
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        _require(slot_mapping.numel() == k_fp16.shape[0], "slot_mapping [T]")
+        ks = _src_rows(k_fp16, "k_fp16", hkv, head_dim)
+        if k_fp16.shape[0] == 0:
+            return
+        dev = _on_gpu(k_fp16, slot_mapping, k_cache, k_scale)
+        rc = self._lib.k8v4_k_store_paged(_ptr(k_fp16), _DTYPE_CODE[k_fp16.dtype], ks, _ptr(slot_mapping),
+                                          int(k_fp16.shape[0]), hkv, head_dim, _ptr(k_cache), _ptr(k_scale),
+                                          int(k_cache.shape[0]), int(k_cache.stride(0)), int(k_scale.stride(0)) * 4,
+                                          _stream(dev))
+        _check(rc, self._lib)
 
-    def v_store_paged(self, *args, **kwargs):
-        raise RuntimeError("v_store_paged: use kv_store_paged (K and V are written by one kernel)")
+    def v_store_paged(self, v_fp16, slot_mapping, v_cache, v_scale, v_zero):
+        """The V half of :meth:`kv_store_paged` (xe2_kv_ops.cpp:1391-1409)."""
+        _require(v_fp16.dim() == 3 and int(v_fp16.shape[2]) in (128, 256), "v_fp16 [T,HKV,D] with D in (128, 256)")
+        head_dim = int(v_fp16.shape[2])
+        _require(slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous(), "slot_mapping int64")
+        hkv = _checked_hkv(int(v_fp16.shape[1]))
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        _require(slot_mapping.numel() == v_fp16.shape[0], "slot_mapping [T]")
+        vs = _src_rows(v_fp16, "v_fp16", hkv, head_dim)
+        if v_fp16.shape[0] == 0:
+            return
+        dev = _on_gpu(v_fp16, slot_mapping, v_cache, v_scale, v_zero)
+        rc = self._lib.k8v4_v_store_paged(_ptr(v_fp16), _DTYPE_CODE[v_fp16.dtype], vs, _ptr(slot_mapping),
+                                          int(v_fp16.shape[0]), hkv, head_dim, _ptr(v_cache), _ptr(v_scale),
+                                          _ptr(v_zero), int(v_cache.shape[0]), int(v_cache.stride(0)),
+                                          int(v_scale.stride(0)) * 4, int(v_zero.stride(0)) * 4, _stream(dev))
+        _check(rc, self._lib)
+
+    # -- the Q-once tile and the ops that read it ----------------------------
+    def q_quant_once(self, q_fp16, q8, q_scale):
+        """Quantize the padded query tile ``[HKV, 64, D]`` into ``q8`` / ``q_scale`` (xe2_kv_ops.cpp:1248-1265)."""
+        _require(q_fp16.dtype in (torch.float16, torch.bfloat16), "q_fp16 must be float16 or bfloat16")
+        _require(q_fp16.dim() == 3 and q_fp16.shape[1] == PAGE and int(q_fp16.shape[2]) in (128, 256),
+                 "q_fp16 shape [HKV,64,D]")
+        _require(q_fp16.is_contiguous(), "q_fp16 must be contiguous")
+        hkv = _checked_hkv(int(q_fp16.shape[0]))
+        self._quantize_tile(q_fp16, Q_PADDED, 0, 0, hkv, int(q_fp16.shape[2]), q8, q_scale)
+
+    def _quantize_tile(self, q, layout, tok_stride, ntok, hkv, head_dim, q8, q_scale):
+        _require(q8.dtype == torch.int8, "q8 must be int8")
+        _require(q_scale.dtype == torch.float32, "q_scale must be float32")
+        _require(q8.is_contiguous() and q8.numel() == hkv * PAGE * head_dim, "q8 numel [HKV,64,D]")
+        _require(q_scale.is_contiguous() and q_scale.numel() == hkv * PAGE, "q_scale numel [HKV,64]")
+        dev = _on_gpu(q, q8, q_scale)
+        rc = self._lib.k8v4_q_quant(_ptr(q), _DTYPE_CODE[q.dtype], layout, tok_stride, ntok, hkv, head_dim,
+                                    _ptr(q8), _ptr(q_scale), _stream(dev))
+        _check(rc, self._lib)
+
+    def int8k_int4v_s1_paged(self, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, seq_lens,
+                             out):
+        """One sequence over the paged cache from a Q-once tile, workspace owned by
+        the library (the reference's legacy op, xe2_kv_ops.cpp:1628-1639)."""
+        self.int8k_int4v_s1_varlen_paged(q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, block_table,
+                                         seq_lens, None, None, None, None, None, out, 1)
+
+    def int8k_int4v_s1_varlen_paged(self, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, block_table,
+                                    seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws, out,
+                                    pages_per_block: int = 1):
+        """One sequence from a Q-once tile with optional explicit causal ends and a
+        caller workspace (xe2_kv_ops.cpp:1641-1660).  ``out`` is ``[Tq, HQ, D]``;
+        Tq is the query length.  ``m_ws``, ``l_ws`` and ``merged_ws`` are accepted
+        and unused; ``partials_ws`` holds the split states (None: the library's
+        own buffer, as the reference's legacy op keeps one)."""
+        del m_ws, l_ws, merged_ws
+        _require(q8.dtype == torch.int8, "q8 int8")
+        _require(q_scale.dtype == torch.float32, "q_scale float32")
+        _require(k_cache.dim() == 4, "k_cache [num_blocks,64,HKV,D] NHD")
+        hkv = _checked_hkv(int(k_cache.shape[2]))
+        head_dim = int(k_cache.shape[3])
+        _require(head_dim in (128, 256), "k_cache head dim must be 128 or 256")
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        _require(k_cache.shape[0] == v_cache.shape[0], "k/v num_blocks")
+        _require(q8.is_contiguous() and q8.numel() == hkv * PAGE * head_dim, "q8 unique [HKV,64,D]")
+        _require(q_scale.is_contiguous() and q_scale.numel() == hkv * PAGE, "q_scale numel [HKV,64]")
+        _require(block_table.dtype == torch.int32, "block_table int32")
+        row = block_table if block_table.dim() == 1 else block_table.reshape(-1, block_table.shape[-1])[0]
+        _require(row.numel() > 0 and row.is_contiguous(), "block_table n_splits")
+        _require(seq_lens.dtype == torch.int32 and seq_lens.numel() >= 1 and seq_lens.is_contiguous(),
+                 "seq_lens int32")
+        _require(out.dim() == 3 and out.shape[1] == GQA * hkv and out.shape[2] == head_dim, "out [Tq,HQ,D]")
+        _require(out.dtype in (torch.float16, torch.bfloat16, torch.float32), "out float32 or float16")
+        _require(out.stride(2) == 1 and out.stride(1) == head_dim, "out head/dim strides")
+        tq = int(out.shape[0])
+        _require(tq > 0 and tq * GQA <= PAGE, "Tq*GQA must fit BM=64 pad")
+        vis_ptr, vis_stride = 0, 0
+        if visible_lens is not None and visible_lens.numel() > 0:
+            _require(visible_lens.dtype == torch.int32 and visible_lens.numel() >= tq + 1 and
+                     visible_lens.is_contiguous(), "visible_lens int32 [1+Tq]")
+            vis_ptr, vis_stride = _ptr(visible_lens), tq + 1
+        ppb = max(1, int(pages_per_block))
+        dev = _on_gpu(q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, row, seq_lens, out)
+        need = self.attn_workspace_bytes(1, int(row.numel()), ppb, tq, hkv, head_dim)
+        if partials_ws is None:
+            ws = self._own_workspace(dev, need)
+        else:
+            _require(partials_ws.is_contiguous() and partials_ws.device == dev, "partials_ws must be a contiguous "
+                     "buffer on the cache's device")
+            ws = partials_ws
+        rc = self._lib.k8v4_attn_batch_q8(
+            _ptr(q8), _ptr(q_scale), hkv * PAGE * head_dim, hkv * PAGE,
+            *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
+            _ptr(row), int(row.numel()), int(row.numel()), ppb, _ptr(seq_lens), vis_ptr, vis_stride, 1, tq, hkv,
+            head_dim, _ptr(out), _DTYPE_CODE[out.dtype], int(out.stride(0)) if tq > 1 else GQA * hkv * head_dim,
+            _ptr(ws), int(ws.numel()) * ws.element_size(), 0, _stream(dev))
+        _check(rc, self._lib)
+
+    def _own_workspace(self, dev, nbytes: int) -> torch.Tensor:
+        """The library-owned split-state buffer of the workspace-free legacy op (grows on demand)."""
+        have = self._legacy_ws.get(dev)
+        if have is None or have.numel() * 4 < nbytes:
+            have = self._legacy_ws[dev] = torch.empty(max(4, -(-nbytes // 4)), dtype=torch.int32, device=dev)
+        return have
+
+    def int8k_int4v_s1_varlen_from_q(self, q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
+                                     block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws, out,
+                                     pages_per_block: int = 1):
+        """Quantize ``q_fp16`` into the Q-once tile (token rows ``[T, HQ, D]`` are
+        packed, a padded ``[HKV, 64, D]`` tile is quantized as is), then
+        :meth:`int8k_int4v_s1_varlen_paged` (xe2_kv_ops.cpp:1663-1712)."""
+        _require(q_fp16.dtype in (torch.float16, torch.bfloat16), "q_fp16 must be float16 or bfloat16")
+        _require(k_cache.dim() == 4, "k_cache [num_blocks,64,HKV,D] NHD")
+        hkv = _checked_hkv(int(k_cache.shape[2]))
+        head_dim = int(k_cache.shape[3])
+        if q_fp16.dim() == 3 and q_fp16.shape[1] == GQA * hkv and q_fp16.shape[2] == head_dim:
+            tq = int(q_fp16.shape[0])
+            _require(tq > 0 and tq * GQA <= PAGE, "tq*GQA exceeds BM")
+            _require(q_fp16.stride(2) == 1 and q_fp16.stride(1) == head_dim, "q_fp16 head/dim strides")
+            self._quantize_tile(q_fp16, Q_TOKENS, int(q_fp16.stride(0)) if tq > 1 else GQA * hkv * head_dim, tq,
+                                hkv, head_dim, q8, q_scale)
+        else:
+            _require(q_fp16.numel() == hkv * PAGE * head_dim and q_fp16.is_contiguous(), "q_fp16 numel")
+            self._quantize_tile(q_fp16, Q_PADDED, 0, 0, hkv, head_dim, q8, q_scale)
+        self.int8k_int4v_s1_varlen_paged(q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero, block_table,
+                                         seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws, out,
+                                         pages_per_block)
+
+    def int8k_int4v_decode_step(self, q_fp16, k_fp16, v_fp16, slot_mapping, q8, q_scale, k_cache, k_scale, v_cache,
+                                v_scale, v_zero, block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws,
+                                merged_ws, out):
+        """One decode step of one sequence: store the new K/V, then attend
+        (xe2_kv_ops.cpp:1716-1731)."""
+        self.kv_store_paged(k_fp16, v_fp16, slot_mapping, k_cache, k_scale, v_cache, v_scale, v_zero)
+        self.int8k_int4v_s1_varlen_from_q(q_fp16, q8, q_scale, k_cache, k_scale, v_cache, v_scale, v_zero,
+                                          block_table, seq_lens, visible_lens, partials_ws, m_ws, l_ws, merged_ws,
+                                          out)
+
+    # -- the reference's unpaged single-page stage tests ---------------------
+    _UNPAGED = ("%s: the reference's unpaged single-page op (contiguous [64, 256] K/V rows, per-page partial "
+                "outputs) is a stage test of its own kernels and is not part of this library; use %s")
+
+    def k_store(self, *args, **kwargs):
+        raise RuntimeError(self._UNPAGED % ("k_store", "k_store_paged or kv_store_paged"))
+
+    def v_store(self, *args, **kwargs):
+        raise RuntimeError(self._UNPAGED % ("v_store", "v_store_paged or kv_store_paged"))
+
+    def int8k_int4v_s1(self, *args, **kwargs):
+        raise RuntimeError(self._UNPAGED % ("int8k_int4v_s1", "int8k_int4v_s1_paged"))
 
 
 def ops() -> _Ops:

@@ -122,3 +122,48 @@ def test_ops_layer_raises_without_gpu_tensors(lib):
     with pytest.raises(RuntimeError, match="GPU tensors"):
         ops_api.ops().kv_store_paged(k, k, torch.zeros(3, dtype=torch.int64), v["k"], v["k_scale"], v["v"],
                                      v["v_scale"], v["v_zero"])
+
+
+def test_q_quant_host_checks(lib):
+    p = 0x10000
+    assert lib.k8v4_q_quant(p, 0, 0, 24 * 128, 7, 3, 128, p, p, None) == 1
+    assert "unsupported per-GPU KV head count 3" in lib.k8v4_last_error().decode()
+    assert lib.k8v4_q_quant(p, 0, 0, 24 * 128, 11, 4, 128, p, p, None) == 1
+    assert lib.k8v4_last_error().decode() == "tq*GQA exceeds BM"
+    assert lib.k8v4_q_quant(p, 0, 5, 0, 0, 4, 128, p, p, None) == 1
+    assert "unknown query layout" in lib.k8v4_last_error().decode()
+    assert lib.k8v4_q_quant(p, 2, 1, 0, 0, 4, 128, p, p, None) == 1
+    assert "q dtype" in lib.k8v4_last_error().decode()
+
+
+def test_attn_q8_host_checks(lib):
+    p = 0x10000
+    args = [p, p, 4 * 64 * 128, 4 * 64, p, p, p, p, p, 64, 52224, 52224, 52224, 52224, 52224, p, 32, 32, 1, p,
+            None, 0, 1, 7, 4, 128, p, 0, 24 * 128, p, 1 << 20, 0, None]
+    bad = list(args)
+    bad[0] = None
+    assert lib.k8v4_attn_batch_q8(*bad) == 1 and "null" in lib.k8v4_last_error().decode()
+    bad = list(args)
+    bad[2] = 64 * 128  # one head's tile per sequence: too short
+    assert lib.k8v4_attn_batch_q8(*bad) == 1 and "q8 must be" in lib.k8v4_last_error().decode()
+    bad = list(args)
+    bad[24] = 3
+    assert lib.k8v4_attn_batch_q8(*bad) == 1
+    assert "unsupported per-GPU KV head count 3" in lib.k8v4_last_error().decode()
+
+
+def test_unpaged_stage_ops_raise_with_a_pointer_to_the_paged_ones(lib):
+    o = ops_api.ops()
+    for name, hint in (("k_store", "k_store_paged"), ("v_store", "v_store_paged"),
+                       ("int8k_int4v_s1", "int8k_int4v_s1_paged")):
+        with pytest.raises(RuntimeError, match="%s: the reference's unpaged single-page op.*use %s" % (name, hint)):
+            getattr(o, name)(None, None, None)
+
+
+def test_every_reference_op_name_is_in_the_table(lib):
+    """The schema list of torch.ops.xe2_kv (xe2_kv_ops.cpp:1779-1822)."""
+    names = ["q_quant_once", "k_store", "v_store", "int8k_int4v_s1", "k_store_paged", "v_store_paged",
+             "kv_store_paged", "int8k_int4v_s1_paged", "int8k_int4v_s1_varlen_paged",
+             "int8k_int4v_s1_varlen_from_q", "int8k_int4v_decode_step", "int8k_int4v_attn_batch"]
+    o = ops_api.ops()
+    assert all(callable(getattr(o, n)) for n in names)

@@ -79,14 +79,31 @@ def test_builder_metadata_and_page_ratio():
 def test_page_ratio_and_shape_checks():
     lay = PageLayout(4, 128)
     cache = vllm_cache(2, 128, lay, "cpu")
-    backend._require_page_ratio(cache, 2, lay)
+    backend._check_block_geometry(cache, 2, lay)
     with pytest.raises(RuntimeError, match="pages_per_block 1 does not match the 128-token cache block"):
-        backend._require_page_ratio(cache, 1, lay)
+        backend._check_block_geometry(cache, 1, lay)
     with pytest.raises(RuntimeError, match="is not \\[block, head, token, 204\\]"):
-        backend._require_page_ratio(cache.view(2, 4, 128 * 204), 2, lay)
+        backend._check_block_geometry(cache.view(2, 4, 128 * 204), 2, lay)
     with pytest.raises(RuntimeError, match="one packed tensor"):
-        backend._one_cache([cache, cache])
-    assert backend._one_cache((cache,)) is cache
+        backend._cache_tensor([cache, cache])
+    assert backend._cache_tensor((cache,)) is cache
+
+
+def test_step_plan_splits_decode_runs_and_prefill_sequences():
+    """The builder plans a step once: runs of 1..10 query tokens are batched
+    decode launches, longer queries one prefill launch per sequence."""
+    runs, seqs = backend.plan_step((0, 7, 14, 21))
+    assert runs == (backend.DecodeRun(0, 3, 7, 0),) and seqs == ()
+    # decode q=1 x2, a 50-token prefill, decode q=1, an empty request, two 12-token prefills
+    starts = (0, 1, 2, 52, 53, 53, 65, 77)
+    runs, seqs = backend.plan_step(starts)
+    assert runs == (backend.DecodeRun(0, 2, 1, 0), backend.DecodeRun(3, 1, 1, 52))
+    assert seqs == (backend.PrefillSeq(2, 2, 50), backend.PrefillSeq(5, 53, 12), backend.PrefillSeq(6, 65, 12))
+    b = make_builder()
+    table = torch.zeros((7, 4), dtype=torch.int32)
+    meta = b.build(0, common_metadata([1, 1, 50, 1, 0, 12, 12], [10, 20, 60, 30, 5, 100, 100], table,
+                                      torch.zeros(77, dtype=torch.int64), "cpu"))
+    assert meta.decode_runs == runs and meta.prefill_seqs == seqs and meta.packed_q_len == 0
 
 
 def test_forward_refuses_output_scale_and_layout_mismatch():
@@ -120,13 +137,42 @@ def test_store_argument_checks():
 
 
 def test_heads_views_of_vllm_rows():
-    lay = PageLayout(4, 128)
     qkv = torch.zeros((3, (24 + 8) * 128))
     q = qkv[:, : 24 * 128]
-    v = backend._heads_view(q, lay, "query")
+    v = backend._rows(q, 24, 128, "query")
     assert v.shape == (3, 24, 128) and v.data_ptr() == q.data_ptr() and v.stride(0) == 32 * 128
-    k = backend._kv_view(qkv[:, 24 * 128 : 28 * 128], lay, "key")
+    k = backend._rows(qkv[:, 24 * 128 : 28 * 128], 4, 128, "key")
     assert k.shape == (3, 4, 128) and k.stride() == (32 * 128, 128, 1)
     with pytest.raises(RuntimeError, match="is not \\[T, 24, 128\\]"):
-        backend._heads_view(torch.zeros((3, 100)), lay, "query")
+        backend._rows(torch.zeros((3, 100)), 24, 128, "query")
     assert math.isclose(backend.attention_pages(2112, None), 33)
+
+
+@pytest.mark.parametrize("hkv,head,max_model_len,max_seqs,max_batched",
+                         [(4, 128, 4096, 256, 8192), (2, 256, 4096, 256, 8192), (4, 128, 131072, 8, 8192),
+                          (2, 256, 200000, 64, 16384)])
+def test_scratch_covers_every_decode_call_the_engine_can_issue(hkv, head, max_model_len, max_seqs, max_batched):
+    """The decode workspace is sized by the library for the widest call of
+    every query length (a batch of short sequences needs more split states
+    than the reference's pages x heads sizing gave it), and the scratch holds
+    only the two workspaces the kernels use."""
+    from k8v4_v030.ops_api import ops
+    from k8v4_v030.scratch import clear_scratch, get_scratch
+
+    clear_scratch()
+    b = make_builder(hkv=hkv, head=head, max_model_len=max_model_len, max_seqs=max_seqs,
+                     max_batched=max_batched, capture=(1, 2, 4, 8, 16))
+    s = get_scratch(torch.device("cpu"), b.layout)
+    lib = ops()
+    pages = -(-max_model_len // 64) + 1
+    for q_len in range(1, 11):
+        batch = max_seqs
+        need = lib.attn_workspace_bytes(batch, pages, 1, q_len, hkv, head)
+        assert s.decode_ws.numel() * 4 >= need, (q_len, need)
+    assert s.prefill_ws.numel() * 4 >= lib.prefill_workspace_bytes(min(max_batched, pages * 64), min(max_batched, pages * 64), hkv, head)
+    # Tens of MB per device, not the reference's [pages x heads, 64, D] fp32 partials.
+    assert s.nbytes < 200 * 2 ** 20
+    ws, m, l, merged = s.workspace(1)
+    assert ws is s.decode_ws and m is None and l is None and merged is None
+    assert s.q8.shape == (hkv, 64, head) and s.q_scale.shape == (hkv, 64)  # created on first use
+    clear_scratch()

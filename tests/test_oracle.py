@@ -252,3 +252,63 @@ def test_prefill_equals_sdpa_bottom_right():
     rows = np.array([0, 17, 39])
     sub = attention.prefill_attention(q, blob, geom, table[0], L, ppb, 1 / math.sqrt(128), rows=rows)
     np.testing.assert_allclose(sub, got[rows], atol=1e-12)
+
+
+# ---------------------------------------------------------------- torch CPU baseline
+def test_torch_cpu_store_writes_the_oracle_bytes():
+    """The CPU baseline's vectorized store (bench.py's cpu_baseline) is bit-exact
+    to the oracle's, including exact ties, constant rows, skipped slots and bf16 input."""
+    import torch
+
+    from oracle import torch_cpu
+
+    geom = paged.Geometry(4, 128)
+    rng = np.random.default_rng(33)
+    key = (rng.standard_normal((90, 4, 128)) * 3).astype(np.float16)
+    value = rng.standard_normal((90, 4, 128)).astype(np.float16)
+    key[5, 1, :4] = [127.0, 0.5, 1.5, -0.5]
+    key[5, 1, 4:] = 0
+    value[6, 2] = 1.25  # constant row: scale floor 1e-8
+    key[7] = 0  # zero rows: codes 0, scale 0
+    slots = rng.permutation(4 * 64)[:90].astype(np.int64)
+    slots[3], slots[4] = -1, 4 * 64 + 9
+    want = paged.new_blob(4, geom)
+    paged.store(want, geom, key, value, slots)
+    raw = torch.zeros(4 * geom.page_bytes, dtype=torch.uint8)
+    torch_cpu.store(torch_cpu.region_views(raw, geom), torch.from_numpy(key), torch.from_numpy(value),
+                    torch.from_numpy(slots))
+    assert np.array_equal(raw.numpy(), want)
+    bf = torch.from_numpy(key.astype(np.float32)).to(torch.bfloat16)
+    want_bf = paged.new_blob(4, geom)
+    paged.store(want_bf, geom, bf.float().numpy(), value, slots)
+    raw.zero_()
+    torch_cpu.store(torch_cpu.region_views(raw, geom), bf, torch.from_numpy(value), torch.from_numpy(slots))
+    assert np.array_equal(raw.numpy(), want_bf)
+
+
+def test_torch_cpu_decode_and_prefill_match_the_oracle():
+    """fp32 torch decode (int8 Q) and key-tiled prefill agree with the float64
+    oracle; a 64-token key tile makes the prefill cross many tiles and row groups."""
+    import torch
+
+    from oracle import torch_cpu
+
+    geom = paged.Geometry(2, 256)
+    rng = np.random.default_rng(34)
+    lengths = [700, 65, 0, 300]
+    blob, table, _ = _random_cache(geom, lengths, rng, ppb=2)
+    views = torch_cpu.region_views(torch.from_numpy(blob.copy()), geom)
+    q = rng.standard_normal((4 * 7, 12, 256)).astype(np.float16)
+    want = attention.decode_attention(q, blob, geom, table, lengths, 7, 2)
+    got = torch_cpu.decode(views, torch.from_numpy(q), torch.from_numpy(table), lengths, 7, 2)
+    np.testing.assert_allclose(got.numpy(), want, atol=2e-5, rtol=1e-4)
+    qp = rng.standard_normal((300, 12, 256)).astype(np.float16)
+    scale = 1 / math.sqrt(256)
+    want_p = attention.prefill_attention(qp, blob, geom, table[0], 700, 2, scale)
+    old = torch_cpu.KEY_TILE, torch_cpu.ROW_GROUP
+    try:
+        torch_cpu.KEY_TILE, torch_cpu.ROW_GROUP = 64, 96
+        got_p = torch_cpu.prefill(views, torch.from_numpy(qp), torch.from_numpy(table[0]), 700, scale, 2)
+    finally:
+        torch_cpu.KEY_TILE, torch_cpu.ROW_GROUP = old
+    np.testing.assert_allclose(got_p.numpy(), want_p, atol=2e-5, rtol=1e-4)
