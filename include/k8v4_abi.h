@@ -199,6 +199,31 @@ int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const i
                        float scale, void *out, int out_dtype, int64_t out_tok_stride,
                        void *workspace, int64_t workspace_bytes, void *stream);
 
+/*
+ * k8v4_attn_batch without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split states go to a library-owned device buffer of
+ * k8v4_attn_noalloc_max_bytes() bytes (32 MiB) per GPU, held until the
+ * process ends; a call whose k8v4_attn_workspace_bytes exceeds it returns
+ * K8V4_ERR_WORKSPACE without launching anything.  The call allocates nothing
+ * (no hipMalloc, no allocating library routine).  All calls on one GPU share
+ * that buffer: calls that overlap on one GPU (other streams, other threads)
+ * race and must not be issued.  Every other argument as k8v4_attn_batch.
+ */
+int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                            const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                            const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                            int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                            int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                            int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                            const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
+                            int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                            int num_splits, void *stream);
+
+/* Bytes of the library-owned split-state buffer of k8v4_attn_batch_noalloc. */
+int64_t k8v4_attn_noalloc_max_bytes(void);
+
 /* Workspace bytes k8v4_prefill_paged needs (0 for q_len == 0, -1 on bad
  * arguments).  No counterpart in the reference (its prefill allocated its
  * gathered K/V per head inside the call, onednn_prefill.py:226-239). */

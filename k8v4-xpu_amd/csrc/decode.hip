@@ -34,6 +34,7 @@
 #include "k8v4_common.h"
 
 #include <cfloat>
+#include <mutex>
 
 namespace k8v4 {
 namespace {
@@ -1401,6 +1402,81 @@ extern "C" int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride,
                           vz_page_stride, block_table, bt_stride, table_width, pages_per_block, seq_lens,
                           visible_lens, vis_stride, batch, q_len, hkv, head_dim, out, out_dtype, out_tok_stride,
                           workspace, workspace_bytes, num_splits, stream, nullptr, 3);
+}
+
+// ------------------------------------------------- allocation-free entry point
+// Split states of k8v4_attn_batch_noalloc: a library-owned device array (one
+// copy per GPU the library runs on, held until the process ends).  Host code
+// reaches it only through the device address hipGetSymbolAddress returns for
+// the current device; the array's name is not a device address on the host.
+// Every call on a GPU shares its copy: calls that overlap on one GPU race.
+// Nothing in it must start at zero (each call writes every split state it
+// reads before reading it).
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace k8v4 {
+namespace {
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64];
+
+// The device address of `scratch` on the current device, resolved once per device.
+int scratch_address(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("k8v4_attn_batch_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return K8V4_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("k8v4_attn_batch_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return K8V4_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return K8V4_OK;
+}
+
+}  // namespace
+}  // namespace k8v4
+
+extern "C" int64_t k8v4_attn_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                                       const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                                       const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                                       int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                                       int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                                       int64_t table_width, int pages_per_block, const int32_t *seq_lens,
+                                       const int32_t *visible_lens, int64_t vis_stride, int64_t batch, int q_len,
+                                       int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
+                                       int num_splits, void *stream) {
+  using namespace k8v4;
+  clear_error();
+  const int64_t need =
+      k8v4_attn_workspace_bytes(batch, table_width, pages_per_block, q_len, hkv, head_dim, num_splits);
+  K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
+  K8V4_REQUIRE(need >= 0, "bad shape for the decode workspace");
+  if (need > kNoAllocScratchBytes) {
+    set_error("k8v4_attn_batch_noalloc: the call needs %lld bytes of split states, the library-owned buffer "
+              "holds %lld (use k8v4_attn_batch with a caller workspace)",
+              static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+    return K8V4_ERR_WORKSPACE;
+  }
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return attn_batch(q, q_dtype, q_tok_stride, nullptr, nullptr, 0, 0, k_cache, k_scale, v_cache, v_scale, v_zero,
+                    num_pages, k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                    block_table, bt_stride, table_width, pages_per_block, seq_lens, visible_lens, vis_stride, batch,
+                    q_len, hkv, head_dim, out, out_dtype, out_tok_stride, ws, kNoAllocScratchBytes, num_splits,
+                    stream, nullptr, 3);
 }
 
 extern "C" int k8v4_attn_batch_q8(const int8_t *q8, const float *q_scale, int64_t q8_seq_stride,
