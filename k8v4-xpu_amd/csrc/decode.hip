@@ -78,6 +78,11 @@ struct DecodeArgs {
   int table_width;
   int ppb;
   const int32_t *seq_lens;
+  // The scale planes share one page stride and lie within 2^30 bytes of
+  // each other: their gathers then use the scalar-base form, with
+  // d_kv = v_scale - k_scale and d_vz = v_zero - v_scale in bytes.
+  int planes_fast;
+  int64_t d_kv, d_vz;
   const int32_t *visible;  // nullable, [batch][vis_stride]
   int64_t vis_stride;
   int batch;
@@ -87,7 +92,10 @@ struct DecodeArgs {
   int64_t split_bytes;  // bytes of one split's state
   int grid;              // number of split work-groups (the plan's G)
   int min_pages;
-  int merge_cs;  // column slices per output row in the merge kernel
+  int merge_cs;   // column slices per output row in the merge
+  int units;      // merge units: output rows x merge_cs
+  int fused;      // the split work-groups also merge (one launch)
+  int *ctr;       // arrival counters of a fused launch (kCtrInts ints)
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -237,6 +245,279 @@ __device__ __forceinline__ int physical_page(const DecodeArgs &a, const int32_t 
   return row[p / a.ppb] * a.ppb + (p % a.ppb);
 }
 
+// ------------------------------------------------------------ merge
+// The splits of one sequence are combined per output row (token, query
+// head): a merge unit is one column slice of one row, VPR = D / 8 / merge_cs
+// columns of 8 dims, folded over the sequence's split states by TPU = 128
+// threads.
+// Thread t owns column t % VPR and the splits t / VPR + k * SPI
+// (SPI = TPU / VPR); it loads the (m, l, O) of up to MU of its splits at
+// once and folds them online (running max, rescaled sums), one round trip per
+// MU splits; the per-thread partial states are then combined in LDS with the
+// same rescaling.
+//
+// The split states are written and read with agent-scope coherent accesses
+// (the sc1 bit: what relaxed agent-scope atomics compile to), so a merge
+// work-group of the same launch can read them as soon as the splits have
+// counted themselves in; no L2 writeback or invalidate is needed.
+//
+// Arrival counters of a fused launch (the splits merge the sequence rows
+// themselves) live in a library-owned pool of blocks, zero when the library
+// is loaded.  In one block, for each slot s (the sequences b with
+// b % kCtrSlots == s), each on a cache line of its own: arrive(s) counts the
+// splits whose state is written, gen(s) counts the launches whose splits all
+// arrived.  A split reads gen when it starts; the last split to arrive
+// returns arrive to zero and bumps gen, which releases the others (a
+// sense-reversing barrier: nothing is left to reset at the end).
+constexpr int kMergeTPU = 128;
+constexpr int kCtrSlots = 64;
+constexpr int kCtrLine = 32;  // ints per 128-byte line
+constexpr int kCtrInts = 2 * kCtrSlots * kCtrLine;
+__device__ __forceinline__ int *ctr_arrive(const DecodeArgs &a, int b) {
+  return a.ctr + (b % kCtrSlots) * kCtrLine;
+}
+__device__ __forceinline__ int *ctr_gen(const DecodeArgs &a, int b) {
+  return a.ctr + (kCtrSlots + b % kCtrSlots) * kCtrLine;
+}
+// A merging split waits at most this many polls (about a second) for the
+// other splits of its sequence; past it, its outputs are NaN.
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
+  if (dtype == K8V4_F32)
+    static_cast<float *>(out)[idx] = v;
+  else if (dtype == K8V4_BF16)
+    static_cast<__bf16 *>(out)[idx] = static_cast<__bf16>(v);
+  else
+    static_cast<_Float16 *>(out)[idx] = static_cast<_Float16>(v);
+}
+
+__device__ __forceinline__ float load_coherent(const float *p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint64_t load_coherent64(const void *p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A store of more than 64 bits reads its data registers in the cycles after
+// issue: the statement waits them out itself, since the compiler's hazard
+// checks do not see inside inline assembly.
+__device__ __forceinline__ void store_coherent16(void *p, v4i v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_coherent4(void *p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+
+typedef float v8f __attribute__((ext_vector_type(8)));
+
+// Where one merge unit's row lives.
+struct MergeRow {
+  int b, tok, qh, r, h, slice;
+};
+__device__ __forceinline__ MergeRow merge_row(const DecodeArgs &a, int unit) {
+  MergeRow m;
+  const int hq = kGqa * a.hkv;
+  const int row_id = unit / a.merge_cs;
+  m.slice = unit - row_id * a.merge_cs;
+  m.qh = row_id % hq;
+  m.tok = row_id / hq;  // b * q_len + j
+  m.b = m.tok / a.q_len;
+  m.h = m.qh / kGqa;
+  m.r = (m.tok - m.b * a.q_len) * kGqa + (m.qh - m.h * kGqa);
+  return m;
+}
+
+// LDS of one merge unit: TPU partial outputs, then SPI running maxima and sums.
+template <int TPU>
+constexpr int merge_lds_bytes() { return TPU * 32 + 2 * TPU * 4; }
+
+// Phase 1: fold this thread's splits and leave its partial state in LDS.
+template <int D, int TPU>
+__device__ void merge_fold(const DecodeArgs &a, int unit, int t, int first, int count, char *red) {
+  constexpr int MU = 8;  // splits loaded together by one thread
+  const int VPR = (D / 8) / a.merge_cs;
+  const int SPI = TPU / VPR;
+  const int col = t % VPR, sg = t / VPR;
+  v8f *red_o = reinterpret_cast<v8f *>(red);
+  float *red_m = reinterpret_cast<float *>(red + TPU * 32);
+  float *red_l = red_m + TPU;
+  float M = -INFINITY, lacc = 0.f;
+  v8f acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (unit >= 0) {
+    const MergeRow mr = merge_row(a, unit);
+    const int rows = a.q_len * kGqa;
+    const int dcol = 8 * (mr.slice * VPR + col);
+    // Byte offsets inside one split state (layout written by the split kernel).
+    const int64_t o_off = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
+    const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
+    const int64_t l_off = m_off + a.hkv * rows * 4;
+    const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
+    for (int s0 = sg; s0 < count; s0 += MU * SPI) {
+      float ms[MU], ls[MU];
+      v8f os[MU];
+#pragma unroll
+      for (int u = 0; u < MU; ++u) {
+        const int s = s0 + u * SPI;
+        ms[u] = -INFINITY;
+        ls[u] = 0.f;
+        os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (s < count) {
+          const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
+          ms[u] = load_coherent(reinterpret_cast<const float *>(st + m_off));
+          ls[u] = load_coherent(reinterpret_cast<const float *>(st + l_off));
+          const uint64_t o0 = load_coherent64(st + o_off), o1 = load_coherent64(st + o_off + 8);
+          const v8h oh = __builtin_bit_cast(v8h, (v4i){static_cast<int>(o0), static_cast<int>(o0 >> 32),
+                                                       static_cast<int>(o1), static_cast<int>(o1 >> 32)});
+          os[u] = __builtin_convertvector(oh, v8f);
+        }
+      }
+      float mn = M;
+#pragma unroll
+      for (int u = 0; u < MU; ++u) mn = fmaxf(mn, ms[u]);
+      if (mn != -INFINITY) {
+        const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
+        lacc *= c;
+        acc *= c;
+#pragma unroll
+        for (int u = 0; u < MU; ++u) {
+          const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
+          lacc += w;
+          acc += (4.f * w) * os[u];
+        }
+        M = mn;
+      }
+    }
+  }
+  red_o[t] = acc;
+  if (col == 0) {
+    red_m[sg] = M;
+    red_l[sg] = lacc;
+  }
+}
+
+// Phase 2 (after a barrier): combine the SPI partial states of each column
+// and store the row's outputs.  `ok` false (a timed-out wait) stores NaN.
+template <int D, int TPU>
+__device__ void merge_finish(const DecodeArgs &a, int unit, int t, bool ok, const char *red) {
+  const int VPR = (D / 8) / a.merge_cs;
+  const int SPI = TPU / VPR;
+  if (unit < 0 || t >= VPR) return;
+  const v8f *red_o = reinterpret_cast<const v8f *>(red);
+  const float *red_m = reinterpret_cast<const float *>(red + TPU * 32);
+  const float *red_l = red_m + TPU;
+  float Mg = -INFINITY;
+  for (int g2 = 0; g2 < SPI; ++g2) Mg = fmaxf(Mg, red_m[g2]);
+  float l = 0.f;
+  v8f o = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (Mg != -INFINITY) {
+    for (int g2 = 0; g2 < SPI; ++g2) {
+      const float mg = red_m[g2];
+      const float w = mg == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg - Mg);
+      l += w * red_l[g2];
+      o += w * red_o[g2 * VPR + t];
+    }
+  }
+  const float inv = !ok ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
+  const MergeRow mr = merge_row(a, unit);
+  const int64_t ob = static_cast<int64_t>(mr.tok) * a.out_tok_stride + static_cast<int64_t>(mr.qh) * D +
+                     8 * (mr.slice * VPR + t);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) store_out(a.out, a.out_dtype, ob + e, o[e] * inv);
+}
+
+// Splits counted on b's slot: those of every sequence sharing it.
+__device__ int slot_splits(const DecodeArgs &a, int P, int b) {
+  int total = 0;
+  for (int bb = b % kCtrSlots; bb < a.batch; bb += kCtrSlots) total += (seq_pages(a, bb) + P - 1) / P;
+  return total;
+}
+
+// The merge of a fused launch, run by the split work-groups themselves once
+// their state is published (the host fuses only when the whole split grid is
+// resident at once, so waiting for the other splits of a sequence cannot
+// block them).  gen0 is gen(b) as read when the split started.  Split s of
+// sequence b (count splits) merges b's units s * UPW + k * count * UPW + grp,
+// UPW units of TPU threads at a time.
+template <int D, int NTH>
+__device__ void merge_in_split(const DecodeArgs &a, int P, int b, int first, int count, int gen0, char *lds) {
+  static_assert(NTH % kMergeTPU == 0, "split work-groups hold whole merge units");
+  constexpr int TPU = kMergeTPU, UPW = NTH / TPU;
+  constexpr int LB = merge_lds_bytes<TPU>();
+  const int tid = threadIdx.x, grp = tid / TPU, t = tid % TPU;
+  const int s = static_cast<int>(blockIdx.x) - first;
+  int *flags = reinterpret_cast<int *>(lds + UPW * LB);
+  // Every wave's state stores have completed at agent scope (each waited for
+  // its own) before the one arrival of this split is counted.
+  __syncthreads();
+  if (tid == 0) {
+    int *arrive = ctr_arrive(a, b);
+    int *gen = ctr_gen(a, b);
+    int ok = 1;
+    if (__hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == slot_splits(a, P, b) - 1) {
+      // The last split of the slot: every other one has arrived and now
+      // polls gen only.
+      __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gen, gen0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      ok = 0;
+      for (int it = 0; it < kSpinLimit; ++it) {
+        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen0) {
+          ok = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    flags[0] = ok;
+  }
+  __syncthreads();
+  const bool ok = flags[0] != 0;
+  const int ub = a.q_len * kGqa * a.hkv * a.merge_cs;  // units of one sequence
+  for (int k0 = s * UPW; k0 < ub; k0 += count * UPW) {
+    const int ul = k0 + grp;
+    const int unit = ul < ub ? b * ub + ul : -1;
+    merge_fold<D, TPU>(a, unit, t, first, count, lds + grp * LB);
+    __syncthreads();
+    merge_finish<D, TPU>(a, unit, t, ok, lds + grp * LB);
+    __syncthreads();
+  }
+}
+
+// Output rows of empty sequences (no split, so no merge): zeros, written in
+// a fused launch by the work-groups the plan leaves idle (an empty sequence
+// takes no split, so there are at least as many idle work-groups as empty
+// sequences).
+template <int D, int NTH>
+__device__ void zero_empty_rows(const DecodeArgs &a, int P, int idle, int nidle) {
+  const int hq = kGqa * a.hkv;
+  int rank = 0;  // empty sequences seen so far
+  for (int bb = 0; bb < a.batch; ++bb) {
+    if (seq_pages(a, bb) > 0) continue;
+    if (rank++ % nidle != idle) continue;
+    const int64_t n = static_cast<int64_t>(a.q_len) * hq * D;
+    for (int64_t e = threadIdx.x; e < n; e += NTH) {
+      const int64_t tok = static_cast<int64_t>(bb) * a.q_len + e / (hq * D);
+      store_out(a.out, a.out_dtype, tok * a.out_tok_stride + e % (hq * D), 0.f);
+    }
+  }
+}
+
+// The merge as a kernel of its own (stage 2 of a staged call): one unit per
+// work-group (the same unit shape as the fused merge, so both give the same
+// bits).
+template <int D>
+__global__ __launch_bounds__(kMergeTPU) void decode_merge_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char red[merge_lds_bytes<kMergeTPU>()];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int unit = static_cast<int>(blockIdx.x);
+  const int P = plan_pages_per_split(a, lane);
+  const SplitRange sr = plan_locate(a, P, lane, merge_row(a, unit).b, -1);
+  merge_fold<D, kMergeTPU>(a, unit, threadIdx.x, sr.first, sr.b < 0 ? 0 : sr.count, red);
+  __syncthreads();
+  merge_finish<D, kMergeTPU>(a, unit, threadIdx.x, true, red);
+}
+
 // ------------------------------------------------------------ split kernel
 //
 // Work-group = NWH waves per KV head.  Wave (h, w) handles KV head h and the
@@ -296,17 +577,42 @@ __device__ __forceinline__ int chunk_token(int g, int i) { return i < 4 ? 4 * g 
 // policy once (1.005x) at the same speed.  The scale planes, shared by the
 // heads of a work-group, and the query rows, shared by the splits of a
 // sequence, also use the default policy.
-constexpr int kPolicyNontemporal = 2;
-
-__device__ __forceinline__ void dma16_nt(const void *src, lds_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0,
-                                   kPolicyNontemporal);
+//
+// The loads use the scalar-base form: a wave-uniform 64-bit base in SGPRs
+// plus a 32-bit per-lane offset, so issuing one costs no vector instruction
+// (the compiler's builtin forms every lane's 64-bit address with vector
+// adds).  Written as inline assembly, these loads are invisible to the
+// compiler's wait counting: every wait on them is explicit (wait_vm), and a
+// compiler-generated wait can only be stronger than needed, never weaker
+// (vector loads complete in issue order); nor does the compiler see LDS
+// being written, which keeps it from waiting for every load in flight before
+// each LDS read.  The compiler's hazard checks do not look inside inline
+// assembly, so the statement sets M0 (the LDS destination) itself and then
+// waits the states the load needs after a scalar write of M0 (1) and after a
+// vector write of an SGPR it reads, such as a v_readfirstlane result in its
+// base (5).
+__device__ __forceinline__ uint32_t lds_addr(const lds_t *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
-__device__ __forceinline__ void dma16(const void *src, lds_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0, 0);
+__device__ __forceinline__ void dma16s_nt(const void *sbase, uint32_t voff, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr(dst))
+               : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void *src, lds_t *dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 4, 0, 0);
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+// Per-lane 64-bit addresses (no scalar base): same statement shape.
+__device__ __forceinline__ void dma4v(const void *addr, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 4\n\tglobal_load_lds_dword %0, off" ::"v"(addr), "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(const void *sbase, uint32_t voff, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr(dst))
+               : "memory", "m0");
 }
 
 // Per-lane byte offsets of one chunk's DMA sources (loop-invariant).
@@ -314,10 +620,14 @@ struct LaneOffsets {
   uint32_t k[4];  // K source per DMA index mod 4: row L/(D/16) of the piece, swizzled chunk
   uint32_t v;     // V: token (lane*16)/VROW (+rows of later DMAs), 16-byte column
   uint32_t s;     // scale plane cell of token (lane & 31)
+  // Scalar-base form of the two scale-plane gathers (when the three planes
+  // share one page stride): offsets from the lower of the two plane bases a
+  // gather reads, lanes 0-31 in the first plane, lanes 32-63 in the second.
+  uint32_t sa, sb;
 };
 
 template <int D, int HKV>
-__device__ __forceinline__ LaneOffsets lane_offsets(int h, int n, int g, int lane) {
+__device__ __forceinline__ LaneOffsets lane_offsets(const DecodeArgs &a, int h, int lane) {
   constexpr int VROW = D / 2, KRP = 1024 / D, CPR = D / 16;
   LaneOffsets o;
 #pragma unroll
@@ -335,6 +645,9 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int h, int n, int g, int lan
     o.v = static_cast<uint32_t>(row * (HKV * VROW) + h * VROW + (lane * 16) % VROW);
   }
   o.s = static_cast<uint32_t>(((lane & 31) * HKV + h) * 4);
+  const int64_t lo_kv = a.d_kv < 0 ? a.d_kv : 0, lo_vz = a.d_vz < 0 ? a.d_vz : 0;
+  o.sa = o.s + static_cast<uint32_t>(lane < 32 ? -lo_kv : a.d_kv - lo_kv);
+  o.sb = o.s + static_cast<uint32_t>(lane < 32 ? -lo_vz : a.d_vz - lo_vz);
   return o;
 }
 
@@ -355,8 +668,7 @@ __device__ __forceinline__ int issue_k(const DecodeArgs &a, const int32_t *bt_ro
   const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps +
                    static_cast<int64_t>(32 * half) * HKV * D;
 #pragma unroll
-  for (int j = 0; j < S::NK; ++j)
-    dma16_nt(kb + static_cast<int64_t>(j) * S::KRP * (HKV * D) + lo.k[j & 3], kslot + j * 1024);
+  for (int j = 0; j < S::NK; ++j) dma16s_nt(kb + static_cast<int64_t>(j) * S::KRP * (HKV * D), lo.k[j & 3], kslot + j * 1024);
   return valid;
 }
 
@@ -371,17 +683,24 @@ __device__ __forceinline__ void issue_v(const DecodeArgs &a, const int32_t *bt_r
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps +
                    static_cast<int64_t>(tok0) * HKV * S::VROW;
 #pragma unroll
-  for (int j = 0; j < S::NV; ++j)
-    dma16(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW) + lo.v, vslot + j * 1024);
-  const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4 + lo.s;
-  const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0;
-  const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0;
-  const char *vzp = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + plane0;
+  for (int j = 0; j < S::NV; ++j) dma16s(vb + static_cast<int64_t>(j) * (1024 / S::VROW) * (HKV * S::VROW), lo.v, vslot + j * 1024);
   // Two full-wave 4-byte DMAs, no divergent branch: ks[32] | vs[32] at
   // S_OFF, then vs[32] | vz[32] at S_OFF + 128 (the v_scale cells are written
   // twice with the same values).
-  dma4(lane < 32 ? ksp : vsp, vslot + S::S_OFF);
-  dma4(lane < 32 ? vsp : vzp, vslot + S::S_OFF + 128);
+  const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4;
+  if (a.planes_fast) {
+    const int64_t lo_kv = a.d_kv < 0 ? a.d_kv : 0, lo_vz = a.d_vz < 0 ? a.d_vz : 0;
+    const char *pa = reinterpret_cast<const char *>(a.k_scale) + lo_kv + phys * a.ks_ps + plane0;
+    const char *pb = reinterpret_cast<const char *>(a.v_scale) + lo_vz + phys * a.vs_ps + plane0;
+    dma4s(pa, lo.sa, vslot + S::S_OFF);
+    dma4s(pb, lo.sb, vslot + S::S_OFF + 128);
+  } else {
+    const char *ksp = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + plane0 + lo.s;
+    const char *vsp = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + plane0 + lo.s;
+    const char *vzp = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + plane0 + lo.s;
+    dma4v(lane < 32 ? ksp : vsp, vslot + S::S_OFF);
+    dma4v(lane < 32 ? vsp : vzp, vslot + S::S_OFF + 128);
+  }
 }
 
 // Wait until at most `after` chunks' DMAs are still in flight.
@@ -658,9 +977,6 @@ struct SplitConfig {
   static constexpr int LDS_MAX = 163840 * HKV / 4;
   static constexpr bool QLDS =
       NWH > 1 || (D == 256 && HKV * Q_LDS_BYTES + WAVES * (2 * Slot<D>::K_BYTES + 2 * Slot<D>::V_BYTES) <= LDS_MAX);
-  // Raw query rows reach LDS-resident fragments through a DMA staging area
-  // in the K ring (two waves per head) or through registers (one wave).
-  static constexpr bool QSTAGE_LDS = NWH > 1;
   static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_LDS_BYTES : 0;
   static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
   // One wave per SIMD (NWH == 1) has no partner wave to cover the table
@@ -682,8 +998,9 @@ struct SplitConfig {
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
   static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
-  // The query rows of a wave's tiles are staged in its K slots 1..RK-1.
-  static_assert(!QSTAGE_LDS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
+  // With two waves per head, the query rows of a wave's tiles are staged in
+  // its K slots 1..RK-1.
+  static_assert(NWH == 1 || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
                 "query staging does not fit the K ring");
 };
 
@@ -705,33 +1022,56 @@ void decode_split_kernel(DecodeArgs a) {
   const int w = wave / HKV;   // position among the NWH waves of this head
   const int n = lane & 15, g = lane >> 4;
 
-  const SplitPlan plan = plan_split(a, lane, static_cast<int>(blockIdx.x));
+  const int role = static_cast<int>(blockIdx.x);  // this work-group's split of the plan
+  const SplitPlan plan = plan_split(a, lane, role);
   const SplitRange sr = plan.r;
-  if (sr.b < 0) return;  // idle work-group (uniform over the work-group)
+  if (sr.b < 0) {
+    // Idle work-group (uniform over the work-group).  In a fused launch the
+    // idle ones write the rows of empty sequences.
+    static_assert(merge_lds_bytes<kMergeTPU>() * (64 * HKV * NWH / kMergeTPU) + 16 <= CFG::LDS_BYTES,
+                  "the merge needs more LDS than the split ring");
+    if (a.fused) {
+      int total = 0;  // splits of the plan
+      for (int b0 = 0; b0 < a.batch; b0 += kWave) {
+        const int bb = b0 + lane;
+        total += bb < a.batch ? (seq_pages(a, bb) + plan.P - 1) / plan.P : 0;
+      }
+      total = wave_sum(total);
+      zero_empty_rows<D, 64 * HKV * NWH>(a, plan.P, role - total, a.grid - total);
+    }
+    return;
+  }
   const int P = plan.P;
   const int b = sr.b;
   const int npages = plan.npages;
   const int L0 = plan.L0;
-  const int p0 = (static_cast<int>(blockIdx.x) - sr.first) * P;
+  const int p0 = (role - sr.first) * P;
   const int p1 = min(npages, p0 + P);
   const int x0 = 2 * p0;
   const int x1 = min(2 * p1, (L0 + 31) / 32);
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
+  // Generation of b's arrival slot (fused launch): a scalar load now, used at
+  // the end; it cannot change before this split has arrived.
+  const int gen0 = a.fused ? ((const_i32_ptr)ctr_gen(a, b))[0] : 0;
 
   // A pre-quantized query tile (k8v4_attn_batch_q8) replaces the raw rows
   // and their quantization below.
   const bool pre_q = a.q8 != nullptr;  // uniform over the launch
 
+  // Query tiles this wave quantizes: all NT of them, except when the NWH
+  // waves of a head share their fragments through LDS (tiles w, w + NWH, ...).
+  constexpr bool QSPLIT = CFG::QLDS && NWH > 1;
+
   // Raw query words.  With Q in registers (one wave per head) they are
   // loaded here, before the ring's first loads, so they do not wait behind
   // them (vector loads complete in order); with Q in LDS they are staged by
   // direct-to-LDS loads further down.
-  uint4 qraw[CFG::QSTAGE_LDS ? 1 : NT][KS][2];
+  v4i qraw[QSPLIT ? 1 : NT][KS][2];
 #pragma unroll
-  for (int nt = 0; nt < (CFG::QSTAGE_LDS ? 0 : NT); ++nt) {
+  for (int nt = 0; nt < (QSPLIT ? 0 : NT); ++nt) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = make_uint4(0u, 0u, 0u, 0u);
+    for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = (v4i){0, 0, 0, 0};
     const int r = 16 * nt + n;
     if (r < rows && !pre_q) {
       const int j = r / kGqa;
@@ -740,30 +1080,30 @@ void decode_split_kernel(DecodeArgs a) {
                             static_cast<int64_t>(qh) * D;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        qraw[nt][ks][0] = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g);
-        qraw[nt][ks][1] = *reinterpret_cast<const uint4 *>(src + 64 * ks + 16 * g + 8);
+        qraw[nt][ks][0] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g);
+        qraw[nt][ks][1] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g + 8);
       }
     }
   }
 
   WaveState<D, NT, CFG::QLDS> st;
   lds_t *qlds = lds + CFG::Q_OFF + h * CFG::Q_BYTES_PER_HEAD;
-  // Causal ends, also read before the first DMAs: row r (token j = r / 6)
-  // sees keys t < lim(r).
+  // Causal ends, through scalar loads (they are uniform over the
+  // work-group): row r (token j = r / 6) sees keys t < lim(r).
   int min_end = L0;
-  for (int j = 0; j < a.q_len; ++j) {
-    const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
-    min_end = min(min_end, e);
-  }
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int r = 16 * nt + n;
-    if (r < rows) {
-      const int j = r / kGqa;
-      const int e = a.visible ? a.visible[static_cast<int64_t>(b) * a.vis_stride + 1 + j] : L0 - a.q_len + j + 1;
-      st.lim[nt] = min(e, L0);
-    } else {
-      st.lim[nt] = L0;
+  for (int nt = 0; nt < NT; ++nt) st.lim[nt] = L0;
+  {
+    const const_i32_ptr vis = a.visible ? (const_i32_ptr)(a.visible + static_cast<int64_t>(b) * a.vis_stride + 1)
+                                        : (const_i32_ptr) nullptr;
+    for (int j = 0; j < a.q_len; ++j) {
+      const int e = a.visible ? vis[j] : L0 - a.q_len + j + 1;
+      min_end = min(min_end, e);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = 16 * nt + n;
+        if (r < rows && r / kGqa == j) st.lim[nt] = min(e, L0);
+      }
     }
   }
 
@@ -772,15 +1112,14 @@ void decode_split_kernel(DecodeArgs a) {
   const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
   lds_t *kring = lds + wave * CFG::WAVE_BYTES;
   lds_t *vring = kring + RK * S::K_BYTES;
-  const LaneOffsets lo = lane_offsets<D, HKV>(h, n, g, lane);
+  const LaneOffsets lo = lane_offsets<D, HKV>(a, h, lane);
   // DMA bookkeeping (wave-uniform): `issued` counts this wave's DMA
   // instructions; mk[s] / mv[s] is the count right after the K / V group of
   // ring slot s was issued, so a chunk is resident once at most
   // issued - max(mk, mv) loads remain outstanding (loads complete in order).
-  // The compiler makes the first use of the Q words wait for every vector
-  // load issued before it, ring DMAs included, so only the first chunk's K
-  // and V groups go out before the quantization; the rest of the ring is
-  // filled right after it.
+  // Only the first chunk's K and V groups go out before the quantization
+  // (register query words wait for every vector load issued before their
+  // first use); the rest of the ring is filled right after it.
   int issued = 0;
   int mk[4] = {0, 0, 0, 0}, mv[4] = {0, 0, 0, 0};
   uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
@@ -804,8 +1143,9 @@ void decode_split_kernel(DecodeArgs a) {
   // a plain count of this wave's own loads.  Rows past the last query row
   // load row 0 and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if (CFG::QSTAGE_LDS && !pre_q) {
+  if (QSPLIT && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
+    const char *qbase = reinterpret_cast<const char *>(a.q) + static_cast<int64_t>(b) * a.q_len * a.q_tok_stride * 2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if (nt % NWH != w) continue;
@@ -816,16 +1156,15 @@ void decode_split_kernel(DecodeArgs a) {
         const int rr = r < rows ? r : 0;
         const int j = rr / kGqa;
         const int qh = h * kGqa + (rr - j * kGqa);
-        const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
-                              static_cast<int64_t>(qh) * D + 8 * (lane % (2 * D / 16));
-        dma16(src, qstage + (ti * 16 + RPD * d) * 2 * D);  // shared by the splits of b: cached
+        const uint32_t off = static_cast<uint32_t>((j * a.q_tok_stride + qh * D + 8 * (lane % (2 * D / 16))) * 2);
+        dma16s(qbase, off, qstage + (ti * 16 + RPD * d) * 2 * D);  // shared by the splits of b: cached
         ++issued;
       }
     }
   }
   const int q_done = issued;
   fill_slot(0);
-  if constexpr (CFG::QSTAGE_LDS) wait_vm(issued - q_done);
+  if constexpr (QSPLIT) wait_vm(issued - q_done);
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
@@ -863,25 +1202,25 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      if constexpr (CFG::QLDS) {
-        if (nt % NWH != w) continue;  // the partner wave quantizes this tile
-      }
+      if (QSPLIT && nt % NWH != w) continue;  // the partner wave quantizes this tile
+      const bool live = 16 * nt + n < rows;
       float x[KS][16];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        uint4 w0, w1;
-        if constexpr (CFG::QSTAGE_LDS) {
+        const v4i zero = {0, 0, 0, 0};
+        v4i w0, w1;
+        if constexpr (QSPLIT) {
           const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
-          const bool live = 16 * nt + n < rows;
-          const v4i r0 = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row);
-          const v4i r1 = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16);
-          w0 = live ? make_uint4(r0[0], r0[1], r0[2], r0[3]) : make_uint4(0u, 0u, 0u, 0u);
-          w1 = live ? make_uint4(r1[0], r1[1], r1[2], r1[3]) : make_uint4(0u, 0u, 0u, 0u);
+          w0 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row) : zero;
+          w1 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16) : zero;
         } else {
           w0 = qraw[nt][ks][0];
           w1 = qraw[nt][ks][1];
         }
-        const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const uint32_t words[8] = {static_cast<uint32_t>(w0[0]), static_cast<uint32_t>(w0[1]),
+                                   static_cast<uint32_t>(w0[2]), static_cast<uint32_t>(w0[3]),
+                                   static_cast<uint32_t>(w1[0]), static_cast<uint32_t>(w1[1]),
+                                   static_cast<uint32_t>(w1[2]), static_cast<uint32_t>(w1[3])};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           x[ks][2 * e] = half_bits_to_float(static_cast<uint16_t>(words[e] & 0xFFFFu), a.q_bf16);
@@ -1026,10 +1365,9 @@ void decode_split_kernel(DecodeArgs a) {
       }
     }
     __syncthreads();
-    if (w != 0) return;
     int e = 0;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < (w == 0 ? NT : 0); ++nt) {
       const float m1 = xb[(e++) * kWave + lane];
       const float m0 = st.m_run[nt];
       const float M = fmaxf(m0, m1);
@@ -1059,12 +1397,13 @@ void decode_split_kernel(DecodeArgs a) {
   // dim group), then m and l in fp32.  A dequantized V value is at most
   // 15 * (65504 * 2 / 15) in magnitude, so a quarter of any average of them
   // is a finite fp16; the merge multiplies by 4 again (exact).
-  char *base = a.ws + static_cast<int64_t>(blockIdx.x) * a.split_bytes;
+  // With two waves per head the combined state is in wave w = 0.
+  char *base = a.ws + static_cast<int64_t>(role) * a.split_bytes;
   _Float16 *obase = reinterpret_cast<_Float16 *>(base);
   float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(HKV) * rows * D * 2);
   float *lbase = mbase + HKV * rows;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < (w == 0 ? NT : 0); ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * nt + 4 * g + i;
@@ -1078,129 +1417,17 @@ void decode_split_kernel(DecodeArgs a) {
                          static_cast<_Float16>(st.O[nt][dg][2][i] * f), static_cast<_Float16>(st.O[nt][dg][3][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][4][i] * f), static_cast<_Float16>(st.O[nt][dg][5][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][6][i] * f), static_cast<_Float16>(st.O[nt][dg][7][i] * f)};
-          *reinterpret_cast<v8h *>(dst) = o;
+          store_coherent16(dst, __builtin_bit_cast(v4i, o));
         }
-        if (n == 0) lbase[h * rows + r] = l;
+        if (n == 0) store_coherent4(lbase + h * rows + r, l);
       }
     }
     const int r = 16 * nt + n;
-    if (g == 0 && r < rows) mbase[h * rows + r] = st.m_run[nt];
+    if (g == 0 && r < rows) store_coherent4(mbase + h * rows + r, st.m_run[nt]);
   }
-}
-
-// ------------------------------------------------------------ merge kernel
-// One 256-thread work-group per (output row, column slice): the D/4 columns
-// (four dims each) of a row (token, query head) are cut into `merge_cs` slices of
-// VPR = D/4/merge_cs columns, so a row whose sequence has many splits is
-// spread over several work-groups.  Thread t owns column t % VPR of the
-// slice and the splits s = t / VPR + k * SPI (SPI = 256 / VPR).  It loads the
-// (m, l, O) of up to MU of its splits at once and folds them online (running
-// max, rescaled sums), one round trip per MU splits; the per-thread partial
-// states are then combined in LDS with the same rescaling.
-
-__device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
-  if (dtype == K8V4_F32)
-    static_cast<float *>(out)[idx] = v;
-  else if (dtype == K8V4_BF16)
-    static_cast<__bf16 *>(out)[idx] = static_cast<__bf16>(v);
-  else
-    static_cast<_Float16 *>(out)[idx] = static_cast<_Float16>(v);
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int MU = 8;  // splits loaded together by one thread
-  const int VPR = (D / 4) / a.merge_cs;  // 16-byte columns per slice (>= 8)
-  const int SPI = 256 / VPR;             // split groups per work-group (<= 32)
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int hq = kGqa * a.hkv;
-  const int row_id = blockIdx.x / a.merge_cs;
-  const int slice = blockIdx.x - row_id * a.merge_cs;
-  const int qh = row_id % hq;
-  const int tok = row_id / hq;  // b * q_len + j
-  const int j = tok % a.q_len;
-  const int b = tok / a.q_len;
-  const int h = qh / kGqa;
-  const int rows = a.q_len * kGqa;
-  const int r = j * kGqa + (qh - h * kGqa);
-
-  const int P = plan_pages_per_split(a, lane);
-  const SplitRange sr = plan_locate(a, P, lane, b, -1);
-  const int first = sr.first, count = sr.b < 0 ? 0 : sr.count;
-
-  const int col = tid % VPR, sg = tid / VPR;
-  const int dcol = 4 * (slice * VPR + col);  // first dim of this thread's column
-  // Byte offsets inside one split state (layout written by the split kernel).
-  const int64_t o_off = (static_cast<int64_t>(h * rows + r) * D + dcol) * 2;
-  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (h * rows + r) * 4;
-  const int64_t l_off = m_off + a.hkv * rows * 4;
-  const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
-
-  __shared__ float red_m[32];
-  __shared__ float red_l[32];
-  __shared__ v4f red_o[256];  // [SPI][VPR]
-
-  float M = -INFINITY, lacc = 0.f;
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = sg; s0 < count; s0 += MU * SPI) {
-    float ms[MU], ls[MU];
-    v4f os[MU];
-#pragma unroll
-    for (int u = 0; u < MU; ++u) {
-      const int s = s0 + u * SPI;
-      ms[u] = -INFINITY;
-      ls[u] = 0.f;
-      os[u] = (v4f){0.f, 0.f, 0.f, 0.f};
-      if (s < count) {
-        const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-        // Default-policy loads: the states were written by the split kernel
-        // just before, and nontemporal loads of them measured slower.
-        ms[u] = *reinterpret_cast<const float *>(st + m_off);
-        ls[u] = *reinterpret_cast<const float *>(st + l_off);
-        const v4h oh = *reinterpret_cast<const v4h *>(st + o_off);
-        os[u] = __builtin_convertvector(oh, v4f);
-      }
-    }
-    float mn = M;
-#pragma unroll
-    for (int u = 0; u < MU; ++u) mn = fmaxf(mn, ms[u]);
-    if (mn != -INFINITY) {
-      const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
-      lacc *= c;
-      acc *= c;
-#pragma unroll
-      for (int u = 0; u < MU; ++u) {
-        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
-        lacc += w;
-        acc += (4.f * w) * os[u];
-      }
-      M = mn;
-    }
-  }
-  red_o[tid] = acc;
-  if (col == 0) {
-    red_m[sg] = M;
-    red_l[sg] = lacc;
-  }
-  __syncthreads();
-  if (tid >= VPR) return;
-  float Mg = -INFINITY;
-  for (int g2 = 0; g2 < SPI; ++g2) Mg = fmaxf(Mg, red_m[g2]);
-  float l = 0.f;
-  v4f o = {0.f, 0.f, 0.f, 0.f};
-  if (Mg != -INFINITY) {
-    for (int g2 = 0; g2 < SPI; ++g2) {
-      const float mg = red_m[g2];
-      const float w = mg == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg - Mg);
-      l += w * red_l[g2];
-      o += w * red_o[g2 * VPR + tid];
-    }
-  }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + dcol;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) store_out(a.out, a.out_dtype, ob + e, o[e] * inv);
+  if (!a.fused) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's state stores have completed
+  merge_in_split<D, 64 * HKV * NWH>(a, P, b, sr.first, sr.count, gen0, lds_raw);
 }
 
 template <int D, int NT>
@@ -1215,6 +1442,97 @@ void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
     case 3: decode_split_kernel<D, 3, HKV, waves_per_head<D, 3>()><<<grid, dim3(64 * HKV * waves_per_head<D, 3>()), 0, s>>>(a); break;
     default: decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a); break;
   }
+}
+
+}  // namespace
+}  // namespace k8v4
+
+// Arrival counters of fused decode launches: kCtrBlocks blocks per GPU, zero
+// when the library is loaded, each returned to zero by every launch that
+// uses it.  A launch uses the block of its workspace (blocks are handed to
+// workspaces in turn, the oldest given up first), so launches that may
+// overlap in time — which need distinct workspaces anyway — use distinct
+// blocks.  Host code reaches the pool only through the device address that
+// hipGetSymbolAddress returns for the current device.
+constexpr int kCtrBlocks = 128;
+static __device__ __align__(256) int k8v4_ctr_pool[kCtrBlocks * k8v4::kCtrInts];
+
+namespace k8v4 {
+namespace {
+
+struct CounterPool {
+  int *base = nullptr;
+  const void *owner[kCtrBlocks] = {};
+  int next = 0;
+};
+std::mutex g_ctr_mu;
+CounterPool g_ctr[64];
+
+int counter_block(const void *workspace, int **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("k8v4_attn_batch: no usable current device (%s)", hipGetErrorString(e));
+    return K8V4_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_ctr_mu);
+  CounterPool &pool = g_ctr[dev];
+  if (!pool.base) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(k8v4_ctr_pool));
+    if (e != hipSuccess || !p) {
+      set_error("k8v4_attn_batch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return K8V4_ERR_HIP;
+    }
+    pool.base = static_cast<int *>(p);
+  }
+  int idx = -1;
+  for (int i = 0; i < kCtrBlocks; ++i)
+    if (pool.owner[i] == workspace) idx = i;
+  if (idx < 0) {
+    idx = pool.next;
+    pool.next = (pool.next + 1) % kCtrBlocks;
+    pool.owner[idx] = workspace;
+  }
+  *out = pool.base + static_cast<int64_t>(idx) * kCtrInts;
+  return K8V4_OK;
+}
+
+// Split work-groups the device holds at once (CUs x work-groups per CU),
+// per kernel instance, cached per device.
+template <int D, int NT, int HKV>
+int resident_wgs_of() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cached[dev]) {
+    constexpr int NWH = waves_per_head<D, NT>();
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(decode_split_kernel<D, NT, HKV, NWH>), 64 * HKV * NWH, 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      return 0;
+    cached[dev] = per_cu * device_cus();
+  }
+  return cached[dev];
+}
+
+template <int D, int HKV>
+int resident_of(int nt) {
+  switch (nt) {
+    case 1: return resident_wgs_of<D, 1, HKV>();
+    case 2: return resident_wgs_of<D, 2, HKV>();
+    case 3: return resident_wgs_of<D, 3, HKV>();
+    default: return resident_wgs_of<D, 4, HKV>();
+  }
+}
+
+int resident_split_wgs(int head_dim, int hkv, int nt) {
+  if (head_dim == 128) return hkv == 4 ? resident_of<128, 4>(nt) : resident_of<128, 2>(nt);
+  return hkv == 4 ? resident_of<256, 4>(nt) : resident_of<256, 2>(nt);
 }
 
 // One split's state: per KV head and query row, D fp16 outputs, then m and l.
@@ -1285,6 +1603,7 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
     K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
                  "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
     K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+    K8V4_REQUIRE(q_tok_stride * q_len < (int64_t(1) << 30), "q token stride too large");
   }
   K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim, "out token stride shorter than HQ*D");
   K8V4_REQUIRE(bt_stride >= table_width, "block_table row stride shorter than its width");
@@ -1323,6 +1642,15 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   a.v_scale = v_scale;
   a.v_zero = v_zero;
   a.num_pages = num_pages;
+  {
+    const int64_t dkv = reinterpret_cast<intptr_t>(v_scale) - reinterpret_cast<intptr_t>(k_scale);
+    const int64_t dvz = reinterpret_cast<intptr_t>(v_zero) - reinterpret_cast<intptr_t>(v_scale);
+    const int64_t lim = int64_t(1) << 30;
+    a.planes_fast = ks_page_stride == vs_page_stride && vs_page_stride == vz_page_stride && dkv > -lim &&
+                    dkv < lim && dvz > -lim && dvz < lim;
+    a.d_kv = a.planes_fast ? dkv : 0;
+    a.d_vz = a.planes_fast ? dvz : 0;
+  }
   a.k_ps = k_page_stride;
   a.ks_ps = ks_page_stride;
   a.v_ps = v_page_stride;
@@ -1342,24 +1670,37 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   a.split_bytes = split_bytes;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
+  // The merge: units of 128 threads (one per work-group of a staged merge;
+  // in a fused launch NTH / 128 per split work-group).  The launch is fused
+  // when the whole split grid is resident at once (a merging split then
+  // never waits for a split that cannot start).
   // Column slices per output row: enough that a merge thread folds at most
   // 16 splits of a sequence with the average split count G / batch (one long
   // sequence can own all G splits); one slice per row otherwise, since every
-  // extra work-group repeats the plan.
+  // extra unit repeats the plan.
+  const int nt = (q_len * kGqa + 15) / 16;
+  const int nth = 64 * hkv * ((head_dim == 128 && nt <= 3) ? 2 : 1);  // split work-group size
+  a.fused = stages == 3 && a.grid <= resident_split_wgs(head_dim, hkv, nt);
+  const int tpu = kMergeTPU;
   {
-    const int vpr = head_dim / 4;
+    const int vpr = head_dim / 8;
     const int64_t avg = (a.grid + batch - 1) / batch;
     int cs = 1;
-    while (vpr / cs > 8 && (256 / (vpr / cs)) * 16 < avg) cs *= 2;
+    while (vpr / cs > 4 && (tpu / (vpr / cs)) * 16 < avg) cs *= 2;
     a.merge_cs = cs;
   }
-  K8V4_REQUIRE(batch * q_len * kGqa * hkv * a.merge_cs <= INT32_MAX, "batch too large for one merge launch");
+  K8V4_REQUIRE(batch * q_len * kGqa * hkv * a.merge_cs <= INT32_MAX / 2, "batch too large for one merge launch");
+  a.units = static_cast<int>(batch * q_len * kGqa * hkv * a.merge_cs);
+  a.ctr = nullptr;
+  if (a.fused) {
+    const int rc = counter_block(workspace, &a.ctr);
+    if (rc) return rc;
+  }
   a.out = out;
   a.out_dtype = out_dtype;
   a.out_tok_stride = out_tok_stride;
 
   auto s = static_cast<hipStream_t>(stream);
-  const int nt = (q_len * kGqa + 15) / 16;
   if (stages & 1) {
     if (head_dim == 128) {
       if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
@@ -1376,12 +1717,13 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
       return K8V4_ERR_HIP;
     }
   }
-  if (!(stages & 2)) return K8V4_OK;
-  const dim3 mgrid(static_cast<unsigned>(batch * q_len * kGqa * hkv * a.merge_cs));
+  if (a.fused || !(stages & 2)) return K8V4_OK;
+  // Not fused: the merge as a kernel of its own.
+  const dim3 mgrid(static_cast<unsigned>(a.units));
   if (head_dim == 128)
-    decode_merge_kernel<128><<<mgrid, dim3(256), 0, s>>>(a);
+    decode_merge_kernel<128><<<mgrid, dim3(kMergeTPU), 0, s>>>(a);
   else
-    decode_merge_kernel<256><<<mgrid, dim3(256), 0, s>>>(a);
+    decode_merge_kernel<256><<<mgrid, dim3(kMergeTPU), 0, s>>>(a);
   return launch_status("k8v4_attn_batch merge");
 }
 
