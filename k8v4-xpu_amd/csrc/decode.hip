@@ -47,6 +47,7 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kScoreBias = 0x4B400000;  // bits of 1.5 * 2^23
 // Lazy-rescale threshold (log2 units): the running max m moves only when a
 // score passes it by more than 4, so exp2(score - m) <= 16.  P is carried as
 // exp2(score - m - 2), a quarter of the probability (row sums and outputs
@@ -651,19 +652,18 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const DecodeArgs &a, int h, 
   return o;
 }
 
-// Starts the DMA of chunk x (32 tokens of head h) into `slot`; returns whether
-// the chunk's page is a valid cache page.  An invalid page still issues its
-// loads (from page 0) so every chunk costs the same vmcnt.  K and V move in
+// Starts the DMA of chunk x (32 tokens of head h, in physical page `phys`, -1
+// outside the cache) into `slot`; returns whether the page is a cache page.
+// An invalid page still issues its loads (from page 0) so every chunk costs
+// the same vmcnt.  K and V move in
 // 16-byte-per-lane DMAs from a wave-uniform base plus a 32-bit lane offset;
 // the scale planes of this head are gathered with two 4-byte DMAs (lanes
 // 0-31: k_scale then v_scale, lanes 32-63: v_scale then v_zero).
 template <int D, int HKV>
-__device__ __forceinline__ int issue_k(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
-                                       lds_t *kslot) {
+__device__ __forceinline__ int issue_k(const DecodeArgs &a, int phys, int x, const LaneOffsets &lo, lds_t *kslot) {
   using S = Slot<D>;
-  const int p = x >> 1, half = x & 1;
-  int phys = physical_page(a, bt_row, p);
-  const int valid = (phys >= 0 && phys < a.num_pages) ? 1 : 0;
+  const int half = x & 1;
+  const int valid = phys >= 0 ? 1 : 0;
   if (!valid) phys = 0;
   const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps +
                    static_cast<int64_t>(32 * half) * HKV * D;
@@ -673,12 +673,11 @@ __device__ __forceinline__ int issue_k(const DecodeArgs &a, const int32_t *bt_ro
 }
 
 template <int D, int HKV>
-__device__ __forceinline__ void issue_v(const DecodeArgs &a, const int32_t *bt_row, int x, const LaneOffsets &lo,
-                                        int lane, lds_t *vslot) {
+__device__ __forceinline__ void issue_v(const DecodeArgs &a, int phys, int x, const LaneOffsets &lo, int lane,
+                                        lds_t *vslot) {
   using S = Slot<D>;
-  const int p = x >> 1, half = x & 1;
-  int phys = physical_page(a, bt_row, p);
-  if (phys < 0 || phys >= a.num_pages) phys = 0;
+  const int half = x & 1;
+  if (phys < 0) phys = 0;
   const int tok0 = 32 * half;
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps +
                    static_cast<int64_t>(tok0) * HKV * S::VROW;
@@ -779,7 +778,7 @@ __device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const
 #pragma unroll
   for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) sc[ml][nt] = (v4i){0, 0, 0, 0};
+    for (int nt = 0; nt < NT; ++nt) sc[ml][nt] = (v4i){kScoreBias, kScoreBias, kScoreBias, kScoreBias};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -822,6 +821,14 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
       }
     }
   }
+  // The QK accumulators start at the bits of 1.5 * 2^23, so each reads as the
+  // float 12582912 + dot, exactly (|dot| <= 128 * 127 * 127 < 2^22); one fma
+  // with k_bias = -12582912 * k_scale gives dot * k_scale within 0.75 of a
+  // unit of the dot (the rounding of k_bias) -- against a query quantization
+  // step of about 0.3 * |k| per dim.
+  float kbias[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kbias[i] = -12582912.0f * ksv[i];
   // ---- scores, chunk max, lazy rescale
   float t[2][NT][4];
   float lmx[NT];  // this lane's largest score of each row tile
@@ -833,7 +840,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
     for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = static_cast<float>(sc[ml][nt][i]) * ksv[4 * ml + i];
+        float v = fmaf(__int_as_float(sc[ml][nt][i]), ksv[4 * ml + i], kbias[4 * ml + i]);
         t[ml][nt][i] = v;
       }
     if (__builtin_expect(masked, 0)) {
@@ -1120,6 +1127,33 @@ void decode_split_kernel(DecodeArgs a) {
   // Only the first chunk's K and V groups go out before the quantization
   // (register query words wait for every vector load issued before their
   // first use); the rest of the ring is filled right after it.
+  // Physical pages of this split's run, looked up once: lane l of ptab[i]
+  // holds page p0 + 64 i + l (-1 outside the cache), read back per chunk
+  // with v_readlane (no scalar-cache miss or page division in the loop).
+  // Runs longer than 128 pages look their pages up as they go.
+  const bool tab_vgpr = p1 - p0 <= 128;
+  int ptab[2] = {-1, -1};
+  if (tab_vgpr) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = p0 + 64 * i + lane;
+      if (p < p1) {
+        const int ph = a.ppb <= 1 ? bt_row[p] : bt_row[p / a.ppb] * a.ppb + p % a.ppb;
+        ptab[i] = (ph >= 0 && ph < a.num_pages) ? ph : -1;
+      }
+    }
+  }
+  auto page_of = [&](int x) -> int {  // x: chunk index in the sequence (wave-uniform)
+    const int p = x >> 1;
+    if (tab_vgpr) {
+      const int d = p - p0;
+      const int lo_pg = __builtin_amdgcn_readlane(ptab[0], d & 63);
+      const int hi_pg = __builtin_amdgcn_readlane(ptab[1], d & 63);
+      return d < 64 ? lo_pg : hi_pg;
+    }
+    const int ph = physical_page(a, bt_row, p);
+    return (ph >= 0 && ph < a.num_pages) ? ph : -1;
+  };
   int issued = 0;
   int mk[4] = {0, 0, 0, 0}, mv[4] = {0, 0, 0, 0};
   uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
@@ -1127,12 +1161,12 @@ void decode_split_kernel(DecodeArgs a) {
     if (s >= cnt) return;
     const int xs = my0 + s * NWH;
     if (s < RK) {
-      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, xs, lo, kring + s * S::K_BYTES)) << s;
+      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xs), xs, lo, kring + s * S::K_BYTES)) << s;
       issued += S::NK;
       mk[s] = issued;
     }
     if (s < RV) {
-      issue_v<D, HKV>(a, bt_row, xs, lo, lane, vring + s * S::V_BYTES);
+      issue_v<D, HKV>(a, page_of(xs), xs, lo, lane, vring + s * S::V_BYTES);
       issued += S::NVS;
       mv[s] = issued;
     }
@@ -1314,7 +1348,8 @@ void decode_split_kernel(DecodeArgs a) {
     if (CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + (k + RK) * NWH, lo, kslot));
+      const int xr = my0 + (k + RK) * NWH;
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1325,7 +1360,8 @@ void decode_split_kernel(DecodeArgs a) {
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, bt_row, my0 + (k + RK) * NWH, lo, kslot));
+      const int xr = my0 + (k + RK) * NWH;
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1334,7 +1370,8 @@ void decode_split_kernel(DecodeArgs a) {
     }
     if (k + RV < cnt) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue_v<D, HKV>(a, bt_row, my0 + (k + RV) * NWH, lo, lane, vslot);
+      const int xr = my0 + (k + RV) * NWH;
+      issue_v<D, HKV>(a, page_of(xr), xr, lo, lane, vslot);
       issued += S::NVS;
 #pragma unroll
       for (int s = 0; s < RV; ++s)
