@@ -115,10 +115,6 @@ int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_tok_stride, i
  * workspace: caller-owned device scratch (16-byte aligned) of
  *      workspace_bytes; k8v4_attn_workspace_bytes() gives what a call needs.
  * num_splits: split-K work-groups (0 = about one per CU).
- * One launch when every split-K work-group fits on the device at once (the
- * default split count): the splits merge the rows of their sequence
- * themselves; otherwise a second, merge kernel.  Calls that may run at the
- * same time (different streams) need distinct workspaces.
  * Requires 1 <= q_len and q_len*6 <= 64.
  */
 int k8v4_attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
@@ -149,12 +145,12 @@ int k8v4_attn_batch_q8(const int8_t *q8, const float *q_scale, int64_t q8_seq_st
                        void *workspace, int64_t workspace_bytes, int num_splits, void *stream);
 
 /*
- * k8v4_attn_batch for timing its split and merge apart.  `split_done_event`
+ * k8v4_attn_batch for timing its two kernels apart.  `split_done_event`
  * (a hipEvent_t as void*, or NULL) is recorded on `stream` after the split-K
- * kernel.  `stages` selects the work: 1 = split-K only (fills the workspace,
- * leaves `out` untouched), 2 = merge only, as a kernel of its own (reads the
- * workspace a previous stages=1 call with the same arguments filled), 3 =
- * both, which is exactly k8v4_attn_batch (one launch when it fuses them).  No counterpart in the reference (its S1/S2
+ * kernel.  `stages` selects the kernels: 1 = split-K only (fills the
+ * workspace, leaves `out` untouched), 2 = merge only (reads the workspace a
+ * previous stages=1 call with the same arguments filled), 3 = both, which is
+ * exactly k8v4_attn_batch.  No counterpart in the reference (its S1/S2
  * timing was an environment-driven host-synchronising log inside the op,
  * k8v4_v030/native/xe2_kv_ops.cpp:1603-1621).
  */

@@ -95,8 +95,6 @@ struct DecodeArgs {
   int min_pages;
   int merge_cs;   // column slices per output row in the merge
   int units;      // merge units: output rows x merge_cs
-  int fused;      // the split work-groups also merge (one launch)
-  int *ctr;       // arrival counters of a fused launch (kCtrInts ints)
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -249,40 +247,15 @@ __device__ __forceinline__ int physical_page(const DecodeArgs &a, const int32_t 
 // ------------------------------------------------------------ merge
 // The splits of one sequence are combined per output row (token, query
 // head): a merge unit is one column slice of one row, VPR = D / 8 / merge_cs
-// columns of 8 dims, folded over the sequence's split states by TPU = 128
-// threads.
-// Thread t owns column t % VPR and the splits t / VPR + k * SPI
+// columns of 8 dims, folded over the sequence's split states by the TPU = 128
+// threads of one work-group.  Thread t owns column t % VPR and the splits
+// t / VPR + k * SPI
 // (SPI = TPU / VPR); it loads the (m, l, O) of up to MU of its splits at
 // once and folds them online (running max, rescaled sums), one round trip per
 // MU splits; the per-thread partial states are then combined in LDS with the
 // same rescaling.
-//
-// The split states are written and read with agent-scope coherent accesses
-// (the sc1 bit: what relaxed agent-scope atomics compile to), so a merge
-// work-group of the same launch can read them as soon as the splits have
-// counted themselves in; no L2 writeback or invalidate is needed.
-//
-// Arrival counters of a fused launch (the splits merge the sequence rows
-// themselves) live in a library-owned pool of blocks, zero when the library
-// is loaded.  In one block, for each slot s (the sequences b with
-// b % kCtrSlots == s), each on a cache line of its own: arrive(s) counts the
-// splits whose state is written, gen(s) counts the launches whose splits all
-// arrived.  A split reads gen when it starts; the last split to arrive
-// returns arrive to zero and bumps gen, which releases the others (a
-// sense-reversing barrier: nothing is left to reset at the end).
+
 constexpr int kMergeTPU = 128;
-constexpr int kCtrSlots = 64;
-constexpr int kCtrLine = 32;  // ints per 128-byte line
-constexpr int kCtrInts = 2 * kCtrSlots * kCtrLine;
-__device__ __forceinline__ int *ctr_arrive(const DecodeArgs &a, int b) {
-  return a.ctr + (b % kCtrSlots) * kCtrLine;
-}
-__device__ __forceinline__ int *ctr_gen(const DecodeArgs &a, int b) {
-  return a.ctr + (kCtrSlots + b % kCtrSlots) * kCtrLine;
-}
-// A merging split waits at most this many polls (about a second) for the
-// other splits of its sequence; past it, its outputs are NaN.
-constexpr int kSpinLimit = 1 << 20;
 
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
   if (dtype == K8V4_F32)
@@ -291,23 +264,6 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
     static_cast<__bf16 *>(out)[idx] = static_cast<__bf16>(v);
   else
     static_cast<_Float16 *>(out)[idx] = static_cast<_Float16>(v);
-}
-
-__device__ __forceinline__ float load_coherent(const float *p) {
-  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ uint64_t load_coherent64(const void *p) {
-  return __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A store of more than 64 bits reads its data registers in the cycles after
-// issue: the statement waits them out itself, since the compiler's hazard
-// checks do not see inside inline assembly.
-__device__ __forceinline__ void store_coherent16(void *p, v4i v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store_coherent4(void *p, float v) {
-  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 
 typedef float v8f __attribute__((ext_vector_type(8)));
@@ -365,12 +321,11 @@ __device__ void merge_fold(const DecodeArgs &a, int unit, int t, int first, int 
         os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (s < count) {
           const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-          ms[u] = load_coherent(reinterpret_cast<const float *>(st + m_off));
-          ls[u] = load_coherent(reinterpret_cast<const float *>(st + l_off));
-          const uint64_t o0 = load_coherent64(st + o_off), o1 = load_coherent64(st + o_off + 8);
-          const v8h oh = __builtin_bit_cast(v8h, (v4i){static_cast<int>(o0), static_cast<int>(o0 >> 32),
-                                                       static_cast<int>(o1), static_cast<int>(o1 >> 32)});
-          os[u] = __builtin_convertvector(oh, v8f);
+          // Default-policy loads: the states were written by the split kernel
+          // just before, and nontemporal loads of them measured slower.
+          ms[u] = *reinterpret_cast<const float *>(st + m_off);
+          ls[u] = *reinterpret_cast<const float *>(st + l_off);
+          os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + o_off), v8f);
         }
       }
       float mn = M;
@@ -398,9 +353,9 @@ __device__ void merge_fold(const DecodeArgs &a, int unit, int t, int first, int 
 }
 
 // Phase 2 (after a barrier): combine the SPI partial states of each column
-// and store the row's outputs.  `ok` false (a timed-out wait) stores NaN.
+// and store the row's outputs.
 template <int D, int TPU>
-__device__ void merge_finish(const DecodeArgs &a, int unit, int t, bool ok, const char *red) {
+__device__ void merge_finish(const DecodeArgs &a, int unit, int t, const char *red) {
   const int VPR = (D / 8) / a.merge_cs;
   const int SPI = TPU / VPR;
   if (unit < 0 || t >= VPR) return;
@@ -419,7 +374,7 @@ __device__ void merge_finish(const DecodeArgs &a, int unit, int t, bool ok, cons
       o += w * red_o[g2 * VPR + t];
     }
   }
-  const float inv = !ok ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
   const MergeRow mr = merge_row(a, unit);
   const int64_t ob = static_cast<int64_t>(mr.tok) * a.out_tok_stride + static_cast<int64_t>(mr.qh) * D +
                      8 * (mr.slice * VPR + t);
@@ -427,86 +382,7 @@ __device__ void merge_finish(const DecodeArgs &a, int unit, int t, bool ok, cons
   for (int e = 0; e < 8; ++e) store_out(a.out, a.out_dtype, ob + e, o[e] * inv);
 }
 
-// Splits counted on b's slot: those of every sequence sharing it.
-__device__ int slot_splits(const DecodeArgs &a, int P, int b) {
-  int total = 0;
-  for (int bb = b % kCtrSlots; bb < a.batch; bb += kCtrSlots) total += (seq_pages(a, bb) + P - 1) / P;
-  return total;
-}
-
-// The merge of a fused launch, run by the split work-groups themselves once
-// their state is published (the host fuses only when the whole split grid is
-// resident at once, so waiting for the other splits of a sequence cannot
-// block them).  gen0 is gen(b) as read when the split started.  Split s of
-// sequence b (count splits) merges b's units s * UPW + k * count * UPW + grp,
-// UPW units of TPU threads at a time.
-template <int D, int NTH>
-__device__ void merge_in_split(const DecodeArgs &a, int P, int b, int first, int count, int gen0, char *lds) {
-  static_assert(NTH % kMergeTPU == 0, "split work-groups hold whole merge units");
-  constexpr int TPU = kMergeTPU, UPW = NTH / TPU;
-  constexpr int LB = merge_lds_bytes<TPU>();
-  const int tid = threadIdx.x, grp = tid / TPU, t = tid % TPU;
-  const int s = static_cast<int>(blockIdx.x) - first;
-  int *flags = reinterpret_cast<int *>(lds + UPW * LB);
-  // Every wave's state stores have completed at agent scope (each waited for
-  // its own) before the one arrival of this split is counted.
-  __syncthreads();
-  if (tid == 0) {
-    int *arrive = ctr_arrive(a, b);
-    int *gen = ctr_gen(a, b);
-    int ok = 1;
-    if (__hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == slot_splits(a, P, b) - 1) {
-      // The last split of the slot: every other one has arrived and now
-      // polls gen only.
-      __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gen, gen0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      ok = 0;
-      for (int it = 0; it < kSpinLimit; ++it) {
-        if (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen0) {
-          ok = 1;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-    }
-    flags[0] = ok;
-  }
-  __syncthreads();
-  const bool ok = flags[0] != 0;
-  const int ub = a.q_len * kGqa * a.hkv * a.merge_cs;  // units of one sequence
-  for (int k0 = s * UPW; k0 < ub; k0 += count * UPW) {
-    const int ul = k0 + grp;
-    const int unit = ul < ub ? b * ub + ul : -1;
-    merge_fold<D, TPU>(a, unit, t, first, count, lds + grp * LB);
-    __syncthreads();
-    merge_finish<D, TPU>(a, unit, t, ok, lds + grp * LB);
-    __syncthreads();
-  }
-}
-
-// Output rows of empty sequences (no split, so no merge): zeros, written in
-// a fused launch by the work-groups the plan leaves idle (an empty sequence
-// takes no split, so there are at least as many idle work-groups as empty
-// sequences).
-template <int D, int NTH>
-__device__ void zero_empty_rows(const DecodeArgs &a, int P, int idle, int nidle) {
-  const int hq = kGqa * a.hkv;
-  int rank = 0;  // empty sequences seen so far
-  for (int bb = 0; bb < a.batch; ++bb) {
-    if (seq_pages(a, bb) > 0) continue;
-    if (rank++ % nidle != idle) continue;
-    const int64_t n = static_cast<int64_t>(a.q_len) * hq * D;
-    for (int64_t e = threadIdx.x; e < n; e += NTH) {
-      const int64_t tok = static_cast<int64_t>(bb) * a.q_len + e / (hq * D);
-      store_out(a.out, a.out_dtype, tok * a.out_tok_stride + e % (hq * D), 0.f);
-    }
-  }
-}
-
-// The merge as a kernel of its own (stage 2 of a staged call): one unit per
-// work-group (the same unit shape as the fused merge, so both give the same
-// bits).
+// The merge kernel: one unit per work-group.
 template <int D>
 __global__ __launch_bounds__(kMergeTPU) void decode_merge_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char red[merge_lds_bytes<kMergeTPU>()];
@@ -516,7 +392,7 @@ __global__ __launch_bounds__(kMergeTPU) void decode_merge_kernel(DecodeArgs a) {
   const SplitRange sr = plan_locate(a, P, lane, merge_row(a, unit).b, -1);
   merge_fold<D, kMergeTPU>(a, unit, threadIdx.x, sr.first, sr.b < 0 ? 0 : sr.count, red);
   __syncthreads();
-  merge_finish<D, kMergeTPU>(a, unit, threadIdx.x, true, red);
+  merge_finish<D, kMergeTPU>(a, unit, threadIdx.x, red);
 }
 
 // ------------------------------------------------------------ split kernel
@@ -1032,22 +908,7 @@ void decode_split_kernel(DecodeArgs a) {
   const int role = static_cast<int>(blockIdx.x);  // this work-group's split of the plan
   const SplitPlan plan = plan_split(a, lane, role);
   const SplitRange sr = plan.r;
-  if (sr.b < 0) {
-    // Idle work-group (uniform over the work-group).  In a fused launch the
-    // idle ones write the rows of empty sequences.
-    static_assert(merge_lds_bytes<kMergeTPU>() * (64 * HKV * NWH / kMergeTPU) + 16 <= CFG::LDS_BYTES,
-                  "the merge needs more LDS than the split ring");
-    if (a.fused) {
-      int total = 0;  // splits of the plan
-      for (int b0 = 0; b0 < a.batch; b0 += kWave) {
-        const int bb = b0 + lane;
-        total += bb < a.batch ? (seq_pages(a, bb) + plan.P - 1) / plan.P : 0;
-      }
-      total = wave_sum(total);
-      zero_empty_rows<D, 64 * HKV * NWH>(a, plan.P, role - total, a.grid - total);
-    }
-    return;
-  }
+  if (sr.b < 0) return;  // idle work-group (uniform over the work-group)
   const int P = plan.P;
   const int b = sr.b;
   const int npages = plan.npages;
@@ -1058,9 +919,6 @@ void decode_split_kernel(DecodeArgs a) {
   const int x1 = min(2 * p1, (L0 + 31) / 32);
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
-  // Generation of b's arrival slot (fused launch): a scalar load now, used at
-  // the end; it cannot change before this split has arrived.
-  const int gen0 = a.fused ? ((const_i32_ptr)ctr_gen(a, b))[0] : 0;
 
   // A pre-quantized query tile (k8v4_attn_batch_q8) replaces the raw rows
   // and their quantization below.
@@ -1402,9 +1260,10 @@ void decode_split_kernel(DecodeArgs a) {
       }
     }
     __syncthreads();
+    if (w != 0) return;
     int e = 0;
 #pragma unroll
-    for (int nt = 0; nt < (w == 0 ? NT : 0); ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       const float m1 = xb[(e++) * kWave + lane];
       const float m0 = st.m_run[nt];
       const float M = fmaxf(m0, m1);
@@ -1434,13 +1293,12 @@ void decode_split_kernel(DecodeArgs a) {
   // dim group), then m and l in fp32.  A dequantized V value is at most
   // 15 * (65504 * 2 / 15) in magnitude, so a quarter of any average of them
   // is a finite fp16; the merge multiplies by 4 again (exact).
-  // With two waves per head the combined state is in wave w = 0.
   char *base = a.ws + static_cast<int64_t>(role) * a.split_bytes;
   _Float16 *obase = reinterpret_cast<_Float16 *>(base);
   float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(HKV) * rows * D * 2);
   float *lbase = mbase + HKV * rows;
 #pragma unroll
-  for (int nt = 0; nt < (w == 0 ? NT : 0); ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * nt + 4 * g + i;
@@ -1454,17 +1312,14 @@ void decode_split_kernel(DecodeArgs a) {
                          static_cast<_Float16>(st.O[nt][dg][2][i] * f), static_cast<_Float16>(st.O[nt][dg][3][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][4][i] * f), static_cast<_Float16>(st.O[nt][dg][5][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][6][i] * f), static_cast<_Float16>(st.O[nt][dg][7][i] * f)};
-          store_coherent16(dst, __builtin_bit_cast(v4i, o));
+          *reinterpret_cast<v8h *>(dst) = o;
         }
-        if (n == 0) store_coherent4(lbase + h * rows + r, l);
+        if (n == 0) lbase[h * rows + r] = l;
       }
     }
     const int r = 16 * nt + n;
-    if (g == 0 && r < rows) store_coherent4(mbase + h * rows + r, st.m_run[nt]);
+    if (g == 0 && r < rows) mbase[h * rows + r] = st.m_run[nt];
   }
-  if (!a.fused) return;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's state stores have completed
-  merge_in_split<D, 64 * HKV * NWH>(a, P, b, sr.first, sr.count, gen0, lds_raw);
 }
 
 template <int D, int NT>
@@ -1479,97 +1334,6 @@ void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
     case 3: decode_split_kernel<D, 3, HKV, waves_per_head<D, 3>()><<<grid, dim3(64 * HKV * waves_per_head<D, 3>()), 0, s>>>(a); break;
     default: decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a); break;
   }
-}
-
-}  // namespace
-}  // namespace k8v4
-
-// Arrival counters of fused decode launches: kCtrBlocks blocks per GPU, zero
-// when the library is loaded, each returned to zero by every launch that
-// uses it.  A launch uses the block of its workspace (blocks are handed to
-// workspaces in turn, the oldest given up first), so launches that may
-// overlap in time — which need distinct workspaces anyway — use distinct
-// blocks.  Host code reaches the pool only through the device address that
-// hipGetSymbolAddress returns for the current device.
-constexpr int kCtrBlocks = 128;
-static __device__ __align__(256) int k8v4_ctr_pool[kCtrBlocks * k8v4::kCtrInts];
-
-namespace k8v4 {
-namespace {
-
-struct CounterPool {
-  int *base = nullptr;
-  const void *owner[kCtrBlocks] = {};
-  int next = 0;
-};
-std::mutex g_ctr_mu;
-CounterPool g_ctr[64];
-
-int counter_block(const void *workspace, int **out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= 64) {
-    set_error("k8v4_attn_batch: no usable current device (%s)", hipGetErrorString(e));
-    return K8V4_ERR_HIP;
-  }
-  std::lock_guard<std::mutex> lock(g_ctr_mu);
-  CounterPool &pool = g_ctr[dev];
-  if (!pool.base) {
-    void *p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(k8v4_ctr_pool));
-    if (e != hipSuccess || !p) {
-      set_error("k8v4_attn_batch: hipGetSymbolAddress: %s", hipGetErrorString(e));
-      return K8V4_ERR_HIP;
-    }
-    pool.base = static_cast<int *>(p);
-  }
-  int idx = -1;
-  for (int i = 0; i < kCtrBlocks; ++i)
-    if (pool.owner[i] == workspace) idx = i;
-  if (idx < 0) {
-    idx = pool.next;
-    pool.next = (pool.next + 1) % kCtrBlocks;
-    pool.owner[idx] = workspace;
-  }
-  *out = pool.base + static_cast<int64_t>(idx) * kCtrInts;
-  return K8V4_OK;
-}
-
-// Split work-groups the device holds at once (CUs x work-groups per CU),
-// per kernel instance, cached per device.
-template <int D, int NT, int HKV>
-int resident_wgs_of() {
-  static std::mutex mu;
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!cached[dev]) {
-    constexpr int NWH = waves_per_head<D, NT>();
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(decode_split_kernel<D, NT, HKV, NWH>), 64 * HKV * NWH, 0) !=
-            hipSuccess ||
-        per_cu < 1)
-      return 0;
-    cached[dev] = per_cu * device_cus();
-  }
-  return cached[dev];
-}
-
-template <int D, int HKV>
-int resident_of(int nt) {
-  switch (nt) {
-    case 1: return resident_wgs_of<D, 1, HKV>();
-    case 2: return resident_wgs_of<D, 2, HKV>();
-    case 3: return resident_wgs_of<D, 3, HKV>();
-    default: return resident_wgs_of<D, 4, HKV>();
-  }
-}
-
-int resident_split_wgs(int head_dim, int hkv, int nt) {
-  if (head_dim == 128) return hkv == 4 ? resident_of<128, 4>(nt) : resident_of<128, 2>(nt);
-  return hkv == 4 ? resident_of<256, 4>(nt) : resident_of<256, 2>(nt);
 }
 
 // One split's state: per KV head and query row, D fp16 outputs, then m and l.
@@ -1707,17 +1471,12 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   a.split_bytes = split_bytes;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
-  // The merge: units of 128 threads (one per work-group of a staged merge;
-  // in a fused launch NTH / 128 per split work-group).  The launch is fused
-  // when the whole split grid is resident at once (a merging split then
-  // never waits for a split that cannot start).
-  // Column slices per output row: enough that a merge thread folds at most
-  // 16 splits of a sequence with the average split count G / batch (one long
-  // sequence can own all G splits); one slice per row otherwise, since every
-  // extra unit repeats the plan.
+  // Merge units of 128 threads, one per merge work-group.  Column slices per
+  // output row: enough that a merge thread folds at most 16 splits of a
+  // sequence with the average split count G / batch (one long sequence can
+  // own all G splits); one slice per row otherwise, since every extra unit
+  // repeats the plan.
   const int nt = (q_len * kGqa + 15) / 16;
-  const int nth = 64 * hkv * ((head_dim == 128 && nt <= 3) ? 2 : 1);  // split work-group size
-  a.fused = stages == 3 && a.grid <= resident_split_wgs(head_dim, hkv, nt);
   const int tpu = kMergeTPU;
   {
     const int vpr = head_dim / 8;
@@ -1728,11 +1487,6 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   }
   K8V4_REQUIRE(batch * q_len * kGqa * hkv * a.merge_cs <= INT32_MAX / 2, "batch too large for one merge launch");
   a.units = static_cast<int>(batch * q_len * kGqa * hkv * a.merge_cs);
-  a.ctr = nullptr;
-  if (a.fused) {
-    const int rc = counter_block(workspace, &a.ctr);
-    if (rc) return rc;
-  }
   a.out = out;
   a.out_dtype = out_dtype;
   a.out_tok_stride = out_tok_stride;
@@ -1754,8 +1508,7 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
       return K8V4_ERR_HIP;
     }
   }
-  if (a.fused || !(stages & 2)) return K8V4_OK;
-  // Not fused: the merge as a kernel of its own.
+  if (!(stages & 2)) return K8V4_OK;
   const dim3 mgrid(static_cast<unsigned>(a.units));
   if (head_dim == 128)
     decode_merge_kernel<128><<<mgrid, dim3(kMergeTPU), 0, s>>>(a);
