@@ -11,24 +11,31 @@
 //  * The problem of one KV head is a matrix of q_len * 6 query rows (token
 //    major, the 6 GQA heads of a token adjacent) against seq_len keys.  A
 //    work-group owns a block of rows of one KV head and streams every page of
-//    that head once: direct-to-LDS loads stage the next page's codes while the
-//    current page is computed, then the group converts them into the other
-//    buffer of a two-buffer MFMA tile ring.  Each page is a 64-key tile shared
-//    by all waves (all GQA rows) of the group.
-//  * Dequantization is split so the per-element work is shared by the whole
-//    work-group: K codes become fp16 integers (byte permute into the mantissa
-//    of 1024.0, then subtract 1152) times the token's K scale and the
-//    exp2-domain softmax factor (one fp16 rounding, as a bf16/fp16 dequant
-//    has); V nibbles become exact fp16 subnormals (n * 2^-24 for even dims,
+//    that head once: direct-to-LDS loads stage coming pages' codes while the
+//    current page is computed, and the group dequantizes them into a ring of
+//    MFMA tiles.  Each page is a 64-key tile shared by all waves (all GQA rows)
+//    of the group.
+//  * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_f16 (the 32x32
+//    shape needs half the operand reads per flop of the 16x16 one): the query
+//    row is the MFMA column, so a lane pair owns one row's softmax state and
+//    the score tile is already the B operand of the PV product.
+//  * K codes become fp16 integers (byte permute into the mantissa of 1024.0,
+//    then subtract 1152) times the token's K scale and the exp2-domain
+//    softmax factor (one fp16 rounding, as a bf16/fp16 dequant has).
+//  * Online softmax in the exp2 domain with a lazy rescale (the running max
+//    only moves when a row's max grows by more than 2^2).
+//  * Head dim 128 (run_segment_pp): eight waves in two groups that alternate
+//    between matrix and vector work half a page apart, so each SIMD's matrix
+//    core and vector ALU run side by side.  V is dequantized into the tile
+//    ((nibble - v_zero) * v_scale / 16, one fp16 rounding) and the softmax
+//    row sums come from the PV product itself (an extra MFMA against a ones
+//    row), so the softmax is max, exp2 and one conversion per score.
+//  * Head dim 256 (run_segment): four waves (the register file holds the wider
+//    accumulators) that convert each page together, then multiply.  V
+//    nibbles become exact fp16 subnormals (n * 2^-24 for even dims,
 //    16 n * 2^-24 for odd dims) in a transposed tile, the V scale multiplies
 //    P and the zero point is subtracted once per row at the end:
 //      sum_t p_t (n_t - z_t) s_t = sum_t (p_t s_t) n_t - sum_t (p_t s_t) z_t.
-//  * S^T = K Q^T and O^T = V^T P'^T on v_mfma_f32_32x32x16_f16 (the 32x32
-//    shapes run at twice the rate of the 16x16 ones on gfx950): the query row
-//    is the MFMA column, so a lane pair owns one row's softmax state and the
-//    score tile is already the B operand of the PV product.
-//  * Online softmax in the exp2 domain with a lazy rescale (the running max
-//    only moves when a row's max grows by more than 2^2).
 #include "k8v4_common.h"
 
 #include <algorithm>
@@ -524,12 +531,475 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
     }
 }
 
+// ---- D = 128: two wave groups in ping-pong ----
+// The eight waves form two groups of four, waves w and w + 4 sharing a SIMD,
+// and the groups run half a page apart: while one group's waves issue the
+// matrix products of a page (the PV product of the previous page with its row
+// sums and the QK product of the current one, 36 MFMAs per wave), the other
+// group's waves on the same SIMDs run the vector work (softmax of the page
+// they last multiplied, half of the dequantization of a coming page, and the
+// DMAs).  A work-group barrier ends every phase, so each SIMD always holds one
+// wave in each kind of work and the matrix core and the vector ALU run side by
+// side.
+//
+// Phases t = 0, 1, ...: group 0 runs A(i) at t = 2i and B(i) at t = 2i + 1,
+// group 1 runs B(i - 1) at t = 2i and A(i) at t = 2i + 1, where
+//   A(i) = PV(i - 1), QK(i), then the LDS reads of this group's next
+//          conversion (tile i + 1 + g: page i + 1 + g's staged codes);
+//   B(i) = dequantize half g' = 1 - g of tile i + 1 + g into the ring (from
+//          those registers), group 1 also issues the DMAs of page i + 5, then
+//          softmax(i).
+// Tile q lives in ring slot q % 3 (written at t = 2q - 2 and 2q - 1, last read
+// by PV(q) at t = 2q + 3), staged page q in slot q % 4 of the staging ring
+// (DMA issued at t = 2q - 8, complete by the end of t = 2q - 5: group 1 waits
+// at the end of each A phase for all but the DMAs of its last B phase; read at
+// the ends of t = 2q - 3 and 2q - 2).
+struct PP {
+  static constexpr int D = 128;
+  static constexpr int NW = 8, THREADS = 512, ROWS = 256;
+  static constexpr int DS = D / 16, DT = D / 32;
+  static constexpr int KROW = 2 * D + 16;  // as Tile<128>
+  static constexpr int V_OFF = 64 * KROW;
+  static constexpr int VROW = 144;
+  static constexpr int BUF = V_OFF + D * VROW;
+  // Staging slot: K codes [64][D], V pieces [part][key parity][key pair] x 16 B,
+  // k_scale | v_scale | v_zero planes (64 floats each).
+  static constexpr int SV_OFF = 64 * D;
+  static constexpr int SS_OFF = SV_OFF + 32 * D;
+  static constexpr int STAGE = SS_OFF + 768;
+  static constexpr int STAGE_OFF = 3 * BUF;
+  static constexpr int LDS = STAGE_OFF + 4 * STAGE;
+  static_assert(ROWS == Tile<128>::ROWS && THREADS == Tile<128>::THREADS, "one block shape per head dim");
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert(BUF % 16 == 0 && STAGE % 16 == 0, "16-byte aligned slots");
+};
+
+// The DMAs of this file's ping-pong path are inline assembly in the
+// scalar-base form (a wave-uniform 64-bit base in SGPRs plus a 32-bit lane
+// offset).  The compiler does not see them: it neither waits for them before
+// unrelated LDS reads nor tracks them, so every wait on them is explicit.  The
+// statement sets M0 (the LDS destination) itself and waits the states the
+// load needs after a scalar write of M0 (1) and after a vector write of an
+// SGPR it reads, such as a v_readfirstlane result in its base (5).
+__device__ __forceinline__ uint32_t lds_addr(const lds_t *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(const void *sbase, uint32_t voff, const lds_t *dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+// Work-group barrier after this wave's LDS writes (a bare s_barrier:
+// __syncthreads() would also wait for every DMA in flight).  One statement, so
+// no LDS access can move across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Per-lane constants of one segment's staging and conversion.
+struct PPLane {
+  uint32_t k0, k1, v, s;  // DMA source offsets: K pieces wv and wv + 4, V piece wv, scale cell of key `lane`
+  int kc_src, kc_dst;     // K conversion: staged chunk, tile byte offset
+  int key;                // K conversion: key of the chunk
+  int v_src, v_dst;       // V conversion: staged dword of the even key, tile byte offset of its first row
+  int vkey;               // V conversion: the even key of the pair
+};
+
+__device__ __forceinline__ PPLane pp_lane(const PrefillArgs &a, int gt, int khalf, int vhalf, int lane) {
+  constexpr int D = PP::D;
+  PPLane L;
+  const int wv = gt >> 6;  // wave within the group
+  const int stride = a.hkv * D;
+  L.k0 = static_cast<uint32_t>((8 * wv + (lane >> 3)) * stride + (lane & 7) * 16);
+  L.k1 = L.k0 + static_cast<uint32_t>(32 * stride);
+  L.v = static_cast<uint32_t>((2 * (lane & 31) + (lane >> 5)) * a.hkv * (D / 2) + wv * 16);
+  L.s = static_cast<uint32_t>(lane * a.hkv * 4);
+  // K: chunk c = 256 * khalf + gt holds dims 16 * (c % 8) .. + 15 of key c / 8.
+  const int c = 256 * khalf + gt;
+  L.key = c >> 3;
+  L.kc_src = 16 * c;
+  L.kc_dst = (c >> 3) * PP::KROW + 32 * (c & 7);
+  // V: item gt of the half reads one dword (bytes 8 hv + 4 sub .. + 3 of
+  // piece q, i.e. dims 32 q + 16 hv + 8 sub .. + 7) of the key pair's two
+  // keys and writes those 8 V^T rows.
+  const int pair = gt & 31, sub = (gt >> 5) & 1, hv = (gt >> 6) & 1, q = 2 * vhalf + (gt >> 7);
+  L.v_src = PP::SV_OFF + (q * 64 + pair) * 16 + (2 * hv + sub) * 4;
+  L.vkey = 2 * pair;
+  const int kp = 2 * pair;  // even key; its column swaps bits 2 and 3
+  const int col = (kp & ~12) | ((kp & 4) << 1) | ((kp & 8) >> 1);
+  L.v_dst = PP::V_OFF + (32 * q + 16 * hv + 8 * sub) * PP::VROW + 2 * col;
+  return L;
+}
+
+// DMAs of physical page phys into a staging slot, shared by the four waves of
+// group 1 (wave wv: K pieces wv and wv + 4, V piece wv, and for wv < 3 the
+// scale plane whose base and page stride the caller passes).
+__device__ __forceinline__ void pp_stage(const PrefillArgs &a, int64_t phys, int h, int wv, const PPLane &L,
+                                         const char *plane, int64_t plane_ps, lds_t *stage) {
+  constexpr int D = PP::D;
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + h * D;
+  dma16s(kb, L.k0, stage + 1024 * wv);
+  dma16s(kb, L.k1, stage + 1024 * (wv + 4));
+  const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps + h * (D / 2);
+  dma16s(vb, L.v, stage + PP::SV_OFF + 1024 * wv);
+  if (wv < 3) dma4s(plane + phys * plane_ps + h * 4, L.s, stage + PP::SS_OFF + 256 * wv);
+}
+
+// One lane's inputs of a conversion, read from a staging slot ahead of use:
+// a K chunk (16 codes and their key's k_scale) and a V item (one dword of the
+// pair's even and odd key, their v_scale and v_zero).
+struct PPKIn {
+  uint4 k;
+  float ks;
+};
+struct PPVIn {
+  uint32_t ev, od;
+  float2 vs, vz;
+};
+
+__device__ __forceinline__ PPKIn pp_fetch_k(const char *stage, int kc_src, int key) {
+  PPKIn in;
+  in.k = *reinterpret_cast<const uint4 *>(stage + kc_src);
+  in.ks = reinterpret_cast<const float *>(stage + PP::SS_OFF)[key];
+  return in;
+}
+__device__ __forceinline__ PPVIn pp_fetch_v(const char *stage, const PPLane &L) {
+  PPVIn in;
+  in.ev = *reinterpret_cast<const uint32_t *>(stage + L.v_src);
+  in.od = *reinterpret_cast<const uint32_t *>(stage + L.v_src + 32 * 16);
+  in.vs = *reinterpret_cast<const float2 *>(stage + PP::SS_OFF + 256 + 4 * L.vkey);
+  in.vz = *reinterpret_cast<const float2 *>(stage + PP::SS_OFF + 512 + 4 * L.vkey);
+  return in;
+}
+
+// K chunk of tile page p: fp16 codes times k_scale * c (zero past the sequence).
+__device__ __forceinline__ void pp_emit_k(const PrefillArgs &a, int p, const PPKIn &in, char *buf, int kc_dst, int key) {
+  const float kc = p * 64 + key < a.seq_len ? in.ks * a.c : 0.f;
+  const v2h kc2 = {static_cast<_Float16>(kc), static_cast<_Float16>(kc)};
+  v2h h[8];
+  k_codes_to_f16(in.k.x, h[0], h[1]);
+  k_codes_to_f16(in.k.y, h[2], h[3]);
+  k_codes_to_f16(in.k.z, h[4], h[5]);
+  k_codes_to_f16(in.k.w, h[6], h[7]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] *= kc2;
+  char *row = buf + kc_dst;
+  *reinterpret_cast<uint4 *>(row) = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
+                                               __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
+  *reinterpret_cast<uint4 *>(row + 16) = make_uint4(__builtin_bit_cast(uint32_t, h[4]), __builtin_bit_cast(uint32_t, h[5]),
+                                                    __builtin_bit_cast(uint32_t, h[6]), __builtin_bit_cast(uint32_t, h[7]));
+}
+
+// V item of tile page p, dequantized: each V^T entry is (nibble - v_zero) *
+// v_scale / 16 rounded once to fp16 (a mixed fma on the exact fp16 value
+// 1024 + nibble, or 1024 + 16 * nibble for the high nibble, with float
+// factors).  The 1/16 keeps every V row of fp16 range (and 16 times more) a
+// finite fp16; the output multiplies it back.  Keys past the sequence become
+// zeros.
+__device__ __forceinline__ void pp_emit_v(const PrefillArgs &a, int p, const PPVIn &in, char *buf, const PPLane &L) {
+  const bool live0 = p * 64 + L.vkey < a.seq_len, live1 = p * 64 + L.vkey + 1 < a.seq_len;
+  const float s0 = live0 ? in.vs.x * 0.0625f : 0.f, s1 = live1 ? in.vs.y * 0.0625f : 0.f;
+  const float z0 = live0 ? in.vz.x : 0.f, z1 = live1 ? in.vz.y : 0.f;
+  const float se0 = s0, se1 = s1, ce0 = -(1024.f + z0) * s0, ce1 = -(1024.f + z1) * s1;
+  const float so0 = s0 * 0.0625f, so1 = s1 * 0.0625f, co0 = -(64.f + z0) * s0, co1 = -(64.f + z1) * s1;
+  char *vrow = buf + L.v_dst;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t sel = 0x0C000C00u | ((4u + b) << 16) | b;
+    const uint32_t x = __builtin_amdgcn_perm(in.od, in.ev, sel);  // byte b of both keys
+    const v2h xe = __builtin_bit_cast(v2h, (x & kEvenNib) | 0x64006400u);  // 1024 + n
+    const v2h xo = __builtin_bit_cast(v2h, (x & kOddNib) | 0x64006400u);   // 1024 + 16 n
+    v2h ye, yo;
+    ye[0] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xe[0]), se0, ce0));
+    ye[1] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xe[1]), se1, ce1));
+    yo[0] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xo[0]), so0, co0));
+    yo[1] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xo[1]), so1, co1));
+    *reinterpret_cast<v2h *>(vrow + (2 * b) * PP::VROW) = ye;
+    *reinterpret_cast<v2h *>(vrow + (2 * b + 1) * PP::VROW) = yo;
+  }
+}
+
+// One segment (pages [p_lo, p_hi) of row block rb of KV head h) on the
+// ping-pong schedule.  Same contract as run_segment.
+__device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem, int h, int rb, int p_lo, int p_hi,
+                                               float *part, int tid, int wave, int lane) {
+  constexpr int D = PP::D;
+  const int g = wave >> 2;   // group
+  const int gt = tid & 255;  // thread within the group
+  const int wv = wave & 3;   // wave within the group
+  const int n = p_hi - p_lo;
+  const int nrows = a.q_len * 6;
+  const int row0 = rb * PP::ROWS;
+  lds_t *stage_lds = (lds_t *)(smem + PP::STAGE_OFF);
+  const char *stage = smem + PP::STAGE_OFF;
+  // Group g dequantizes half 1 - g of each tile (K chunks and V items).
+  const PPLane L = pp_lane(a, gt, 1 - g, 1 - g, lane);
+  // The scale plane this wave stages (group 1, waves 0-2 of the group).
+  const char *plane = reinterpret_cast<const char *>(wv == 0 ? a.k_scale : wv == 1 ? a.v_scale : a.v_zero);
+  const int64_t plane_ps = wv == 0 ? a.ks_ps : wv == 1 ? a.vs_ps : a.vz_ps;
+
+  // ---- query fragments (B operand of S^T = K Q^T) and the row limit, as run_segment.
+  const int hh = lane / 32, r32 = lane % 32;
+  const int row = row0 + wave * 32 + r32;
+  const bool row_valid = row < nrows;
+  v8h qf[PP::DS];
+  int lim;
+  {
+    const int tok = row_valid ? row / 6 : 0;
+    const int qh = h * 6 + (row_valid ? row % 6 : 0);
+    lim = row_valid ? a.seq_len - a.q_len + tok + 1 : 1;
+    const uint16_t *src = a.q + static_cast<int64_t>(tok) * a.q_tok_stride + static_cast<int64_t>(qh) * D + 8 * hh;
+    if (a.q_bf16) {
+#pragma unroll
+      for (int ds = 0; ds < PP::DS; ++ds) {
+        const uint4 raw = row_valid ? *reinterpret_cast<const uint4 *>(src + 16 * ds) : make_uint4(0, 0, 0, 0);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qf[ds][2 * e] = static_cast<_Float16>(__uint_as_float(w[e] << 16));
+          qf[ds][2 * e + 1] = static_cast<_Float16>(__uint_as_float(w[e] & 0xFFFF0000u));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ds = 0; ds < PP::DS; ++ds) {
+        const uint4 raw = row_valid ? *reinterpret_cast<const uint4 *>(src + 16 * ds) : make_uint4(0, 0, 0, 0);
+        qf[ds] = __builtin_bit_cast(v8h, raw);
+      }
+    }
+  }
+  const int tok_lo = row0 / 6;
+  const int full_pages = (a.seq_len - a.q_len + tok_lo + 1) / 64;
+
+  v16f O[PP::DT];
+#pragma unroll
+  for (int dt = 0; dt < PP::DT; ++dt) O[dt] = (v16f)0.f;
+  float m_run = -INFINITY;
+  v16f S[2];
+  v8h pb[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) pb[st] = (v8h)0;
+  // Row sums on the matrix core: an A operand whose row 0 is all ones puts
+  // sum_k P[k][r] in row 0 of Lacc (register 0 of lanes 0-31); its other rows
+  // stay zero.
+  v16f Lacc = (v16f)0.f;
+  const v8h ones_a = (v8h)(r32 == 0 ? (_Float16)1.0f : (_Float16)0.0f);  // row 0 (lanes 0 and 32), all 16 keys
+  const int k_base = r32 * PP::KROW + 16 * hh;
+  const int v_base = PP::V_OFF + r32 * PP::VROW + 16 * hh;
+  PPKIn kin;  // inputs of this lane's next K chunk
+  PPVIn vin;  // and of its next V item
+
+  // ---- prologue: pages 0-3 staged, tile 0 dequantized by both groups, group
+  // 1's inputs for tile 1 fetched.
+  if (g == 1) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < n) pp_stage(a, page_of(a, p_lo + q), h, wv, L, plane, plane_ps, stage_lds + q * PP::STAGE);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  lds_barrier();
+  pp_emit_k(a, p_lo, pp_fetch_k(stage, L.kc_src, L.key), smem, L.kc_dst, L.key);
+  pp_emit_v(a, p_lo, pp_fetch_v(stage, L), smem, L);
+  if (g == 1 && n > 1) {
+    kin = pp_fetch_k(stage + PP::STAGE, L.kc_src, L.key);
+    vin = pp_fetch_v(stage + PP::STAGE, L);
+  }
+  lds_barrier();
+
+  // Physical page of group 1's next DMA (looked up in its A phase, where the
+  // scalar load's latency costs no vector work).
+  int64_t next_phys = 0;
+
+  // A(i): PV(i - 1) from tile slot (i - 1) % 3 with its row sums, then QK(i)
+  // from slot i % 3, as one straight run of MFMAs with the operand reads
+  // eight ahead.  Both products always run: PV(-1) multiplies a finite tile
+  // (the ring starts zeroed) by a zero operand, and QK(n) fills scores that
+  // are never read.  Then the inputs of the next conversion are read.
+  auto phase_a = [&](int i, int slot_prev, int slot_cur) {
+    // The wave feeding the matrix core wins issue conflicts with its SIMD's
+    // other wave (the vector work fills the remaining issue slots).
+    __builtin_amdgcn_s_setprio(3);
+    if (g == 1 && i + 5 < n) next_phys = page_of(a, p_lo + i + 5);
+    const char *vbase = smem + slot_prev * PP::BUF + v_base;
+    const char *kbase = smem + slot_cur * PP::BUF + k_base;
+    // operand k: PV (st, dt) = (k / 4, k % 4) for k < 16, QK (ds, mt) = ((k - 16) / 2, k % 2) after
+    auto frag = [&](int k) -> v8h {
+      if (k < 16) return *reinterpret_cast<const v8h *>(vbase + 32 * (k & 3) * PP::VROW + 32 * (k >> 2));
+      const int kk = k - 16;
+      return *reinterpret_cast<const v8h *>(kbase + 32 * (kk & 1) * PP::KROW + 32 * (kk >> 1));
+    };
+    constexpr int AHEAD = 8;
+    v8h f[AHEAD];
+#pragma unroll
+    for (int k = 0; k < AHEAD; ++k) f[k] = frag(k);
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    S[0] = (v16f)(-m_use);
+    S[1] = (v16f)(-m_use);
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      if (k < 16) {
+        O[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k % AHEAD], pb[k >> 2], O[k & 3], 0, 0, 0);
+        if ((k & 3) == 3) Lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_a, pb[k >> 2], Lacc, 0, 0, 0);
+      } else {
+        const int kk = k - 16;
+        S[kk & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k % AHEAD], qf[kk >> 1], S[kk & 1], 0, 0, 0);
+      }
+      if (k + AHEAD < 32) f[k % AHEAD] = frag(k + AHEAD);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      if ((k & 3) == 3 && k < 16)
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      else
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (k + AHEAD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    // Group 1's DMAs older than its last B phase's (page i + 4 and before)
+    // land before the barrier (vector loads complete in issue order); group 0
+    // has none in flight.
+    if (g == 1 && i + 4 < n) {
+      if (wv < 3)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    // Inputs of this group's conversion in B(i): tile i + 1 + g.
+    const int ct = i + 1 + g;
+    if (ct < n) {
+      const char *st = stage + (ct & 3) * PP::STAGE;
+      kin = pp_fetch_k(st, L.kc_src, L.key);
+      vin = pp_fetch_v(st, L);
+    }
+  };
+
+  // Softmax of page i: P = exp2(x - m) as the fp16 B operand of the PV
+  // product (whose ones row also sums these same fp16 values).
+  auto softmax = [&](int i) {
+    const int p = p_lo + i;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    if (__builtin_expect(p >= full_pages, 0)) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (p * 64 + 32 * mt + 8 * j + 4 * hh + e >= lim) S[mt][4 * j + e] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, S[mt][e]);
+    const float thr = m_run == -INFINITY ? -INFINITY : kThreshold;
+    if (__ballot(mx > thr)) {
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      const float rmx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) + m_use;
+      const float mnew = fmaxf(m_run, rmx);
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew);
+      m_run = mnew;
+      Lacc[0] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < PP::DT; ++dt) O[dt] *= alpha;
+      const float delta = m_run == -INFINITY ? 0.f : m_run - m_use;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) S[mt] -= delta;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pb[2 * mt + (j >> 1)][4 * (j & 1) + e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(S[mt][4 * j + e]));
+  };
+
+  // B(i): this group's half of tile i + 1 + g from the fetched inputs, group
+  // 1's DMAs of page i + 5 (four per wave, three in the fourth), then softmax(i).
+  auto phase_b = [&](int i) {
+    __builtin_amdgcn_s_setprio(0);
+    const int ct = i + 1 + g;
+    if (ct < n) {
+      char *buf = smem + (ct % 3) * PP::BUF;
+      pp_emit_k(a, p_lo + ct, kin, buf, L.kc_dst, L.key);
+      pp_emit_v(a, p_lo + ct, vin, buf, L);
+    }
+    if (g == 1 && i + 5 < n) pp_stage(a, next_phys, h, wv, L, plane, plane_ps, stage_lds + ((i + 5) & 3) * PP::STAGE);
+    if (i >= 0 && i < n) softmax(i);
+  };
+
+  // Group 1 starts half a page late: its B(-1) converts and stages only.
+  if (g == 1) {
+    if (n > 4) next_phys = page_of(a, p_lo + 4);
+    phase_b(-1);
+    lds_barrier();
+  }
+  // slot = i % 3 for page i; slot_m1 = (i - 1) % 3.
+  int slot = 0, slot_m1 = 2;
+  for (int i = 0; i <= n; ++i) {
+    phase_a(i, slot_m1, slot);
+    lds_barrier();
+    // Group 1's B(n) would be empty; skipping it keeps both groups at 2n + 2 barriers.
+    if (g == 0 || i < n) {
+      phase_b(i);
+      lds_barrier();
+    }
+    slot_m1 = slot;
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+
+  __builtin_amdgcn_s_setprio(0);
+  // ---- finalize: O = 16 acc / l (row sums from lane r32's Lacc[0]; V^T holds V / 16).
+  float l;
+  {
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(Lacc[0]), __float_as_uint(Lacc[0]), false, false);
+    l = hh == 0 ? Lacc[0] : __uint_as_float(sw[0]);
+  }
+  if (part) {
+    const int lr = wave * 32 + r32;
+#pragma unroll
+    for (int dt = 0; dt < PP::DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4f o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = 16.f * O[dt][4 * j + e];
+        *reinterpret_cast<v4f *>(part + lr * D + 32 * dt + 8 * j + 4 * hh) = o;
+      }
+    if (hh == 0) {
+      part[PP::ROWS * D + lr] = m_run;
+      part[PP::ROWS * D + PP::ROWS + lr] = l;
+    }
+    return;
+  }
+  if (!row_valid) return;
+  const float inv = l > 0.f ? 16.f / l : 0.f;
+  const int tok = row / 6, qh = h * 6 + row % 6;
+  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + 4 * hh;
+#pragma unroll
+  for (int dt = 0; dt < PP::DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v4f o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = O[dt][4 * j + e] * inv;
+      store_out4(a.out, a.out_dtype, ob + 32 * dt + 8 * j, o);
+    }
+}
+
 template <int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(Tile<D>::THREADS, Tile<D>::THREADS),
                           amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
 prefill_kernel(PrefillArgs a) {
   using T = Tile<D>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * T::BUF + T::STAGE];
+  constexpr int LDS_BYTES = D == 128 ? PP::LDS : 2 * T::BUF + T::STAGE;
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
   const int w = blockIdx.x;
   const int v = a.xcd_perm ? (w % 8) * (a.grid / 8) + w / 8 : w;
   const int s0 = range_start(a, v), s1 = range_start(a, v + 1);
@@ -537,6 +1007,10 @@ prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   const int lane = tid % 64;
+  if constexpr (D == 128) {
+    // The ping-pong ring starts zeroed: its tiles then only ever hold finite values.
+    for (int o = 16 * tid; o < PP::STAGE_OFF; o += 16 * PP::THREADS) *reinterpret_cast<uint4 *>(smem + o) = make_uint4(0, 0, 0, 0);
+  }
   int s = s0;
   bool first = true;
   while (s < s1) {
@@ -549,7 +1023,10 @@ prefill_kernel(PrefillArgs a) {
     float *part = nullptr;
     if (p_lo != 0 || p_hi != n)
       part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * T::ROWS * (D + 2);
-    run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+    if constexpr (D == 128)
+      run_segment_pp(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+    else
+      run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     s += p_hi - p_lo;
     first = false;
   }

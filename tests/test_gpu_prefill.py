@@ -169,3 +169,31 @@ def test_prefill_blocks_split_across_many_work_groups(gpu_ops, q_len, seq_len):
     got = _run(cache, q, table[0], seq_len).float().cpu().numpy()
     assert_close(got, _oracle(cache, q, table[0], seq_len), what="split blocks")
     assert gpu_ops.prefill_workspace_bytes(seq_len, q_len, 4, 128) > 0
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_prefill_values_near_the_fp16_limit(gpu_ops, d):
+    """Every 7th token's V row alternates 60000 / -65504 (its -65504 codes
+    dequantize to -8 * 125504 / 15 = -66935, beyond fp16) and its K row draws
+    almost all of the softmax weight, so outputs exceed 65504 in magnitude:
+    the dequantized tiles and the accumulation must stay finite and match the
+    oracle for fp32 output."""
+    print("prefill large V d=%d" % d, flush=True)
+    lay = PageLayout(2, d)
+    cache = Cache(64, lay)
+    gen = torch.Generator().manual_seed(43)
+    L, q_len = 3000, 40
+    table = random_tables(gen, [L], 64)
+    t = torch.arange(L)
+    slots = (table[0].long()[t // PAGE] * PAGE + t % PAGE).to(DEV)
+    k = seeded_normal(gen, (L, 2, d))
+    v = seeded_normal(gen, (L, 2, d))
+    k[::7] = 4.0
+    v[::7, :, 0::2] = 60000.0
+    v[::7, :, 1::2] = -65504.0
+    cache.store(gpu_ops, k.to(DEV), v.to(DEV), slots)
+    q = seeded_normal(gen, (q_len, 12, d)).abs()
+    want = _oracle(cache, q, table[0], L)
+    assert np.abs(want).max() > 65504.0
+    got = _run(cache, q, table[0], L, out_dtype=torch.float32)
+    assert_close(got.cpu().numpy(), want, what="large V d=%d" % d)
