@@ -187,7 +187,9 @@ int k8v4_attn_batch_profiled(const void *q, int q_dtype, int64_t q_tok_stride,
  * workspace: caller-owned device scratch (16-byte aligned) of workspace_bytes
  *      >= k8v4_prefill_workspace_bytes(seq_len, q_len, hkv, head_dim): partial
  *      softmax states of the row blocks the balanced schedule splits between
- *      work-groups.
+ *      work-groups and, for head_dim 128 with q_len * 6 > 768 query rows per
+ *      KV head, one head's pages dequantized into MFMA tile images (35,840
+ *      bytes per 64-token page; the heads run one after another over it).
  * q_len == 0 is a no-op; q_len > seq_len is an error.
  */
 int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,

@@ -80,6 +80,8 @@ struct PrefillArgs {
   int grid;      // persistent work-groups; work-group v takes steps [v*total/grid, (v+1)*total/grid)
   int xcd_perm;  // map ids so the work-groups of one XCD take adjacent work (grid % 8 == 0)
   float *ws;     // partial states: [grid][2][rows][D + 2] floats
+  int head0;     // KV head of step 0 (a launch covers heads head0 .. head0 + total / tper - 1)
+  const char *tiles;  // head dim 128: dequantized tiles of head head0, [page][PP::BUF] bytes (null: convert in-kernel)
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -724,6 +726,15 @@ __device__ __forceinline__ void pp_emit_v(const PrefillArgs &a, int p, const PPV
 
 // One segment (pages [p_lo, p_hi) of row block rb of KV head h) on the
 // ping-pong schedule.  Same contract as run_segment.
+//
+// PRE: the tiles were dequantized beforehand (prefill_convert_kernel writes
+// each page's tile image to a.tiles once for all row blocks): the groups
+// copy them straight into a four-slot ring with DMAs and the B phases hold
+// only the softmax.  Tile q lives in slot q % 4; group 1 issues its pieces of
+// tile q in B(q - 3) (t = 2q - 4) and waits for them at the end of A(q - 1),
+// group 0 issues its pieces in B(q - 2) (t = 2q - 3) and waits at the end of
+// B(q - 1); slot q % 4 was last read by PV(q - 4) at t = 2q - 5.
+template <bool PRE>
 __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem, int h, int rb, int p_lo, int p_hi,
                                                float *part, int tid, int wave, int lane) {
   constexpr int D = PP::D;
@@ -785,29 +796,64 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
   // Row sums on the matrix core: an A operand whose row 0 is all ones puts
   // sum_k P[k][r] in row 0 of Lacc (register 0 of lanes 0-31); its other rows
   // stay zero.
+  // (PRE, where the matrix core is the busier unit: fp32 sums on the vector
+  // ALU instead, two per lane, and the scores start from Minit = -m in the
+  // first k-step's accumulator input, rewritten only when m moves.)
   v16f Lacc = (v16f)0.f;
   const v8h ones_a = (v8h)(r32 == 0 ? (_Float16)1.0f : (_Float16)0.0f);  // row 0 (lanes 0 and 32), all 16 keys
+  float lsum0 = 0.f, lsum1 = 0.f;
+  v16f Minit = (v16f)0.f;
   const int k_base = r32 * PP::KROW + 16 * hh;
   const int v_base = PP::V_OFF + r32 * PP::VROW + 16 * hh;
   PPKIn kin;  // inputs of this lane's next K chunk
   PPVIn vin;  // and of its next V item
 
+  // DMA pieces of one tile (1 KB each, 35 per tile): piece k belongs to group
+  // k % 2, wave (k / 2) % 4 of it.
+  static_assert(PP::BUF % 1024 == 0 && 4 * PP::BUF <= PP::LDS, "tile pieces and four-slot ring");
+  const char *tsrc = PRE ? a.tiles + static_cast<int64_t>(p_lo) * PP::BUF : nullptr;
+  auto tile_dma = [&](int q) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const int k = 2 * (wv + 4 * j) + g;
+      if (k < PP::BUF / 1024)
+        dma16s(tsrc + static_cast<int64_t>(q) * PP::BUF, static_cast<uint32_t>(1024 * k + 16 * lane),
+               (lds_t *)(smem + (q & 3) * PP::BUF + 1024 * k));
+    }
+  };
+  // this wave's pieces per tile: 5 for (g, wv) = (0, 0), (0, 1), (1, 0), else 4
+  const bool five = wv + g < 2;
+  auto wait_older = [&]() {  // all but this wave's pieces of its last tile
+    if (five)
+      asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  };
+  if constexpr (PRE) {
+    tile_dma(0);
+    if (n > 1) tile_dma(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+  }
+
   // ---- prologue: pages 0-3 staged, tile 0 dequantized by both groups, group
   // 1's inputs for tile 1 fetched.
-  if (g == 1) {
+  if (!PRE && g == 1) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (q < n) pp_stage(a, page_of(a, p_lo + q), h, wv, L, plane, plane_ps, stage_lds + q * PP::STAGE);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  lds_barrier();
-  pp_emit_k(a, p_lo, pp_fetch_k(stage, L.kc_src, L.key), smem, L.kc_dst, L.key);
-  pp_emit_v(a, p_lo, pp_fetch_v(stage, L), smem, L);
-  if (g == 1 && n > 1) {
-    kin = pp_fetch_k(stage + PP::STAGE, L.kc_src, L.key);
-    vin = pp_fetch_v(stage + PP::STAGE, L);
+  if constexpr (!PRE) {
+    lds_barrier();
+    pp_emit_k(a, p_lo, pp_fetch_k(stage, L.kc_src, L.key), smem, L.kc_dst, L.key);
+    pp_emit_v(a, p_lo, pp_fetch_v(stage, L), smem, L);
+    if (g == 1 && n > 1) {
+      kin = pp_fetch_k(stage + PP::STAGE, L.kc_src, L.key);
+      vin = pp_fetch_v(stage + PP::STAGE, L);
+    }
+    lds_barrier();
   }
-  lds_barrier();
 
   // Physical page of group 1's next DMA (looked up in its A phase, where the
   // scalar load's latency costs no vector work).
@@ -822,7 +868,7 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
     // The wave feeding the matrix core wins issue conflicts with its SIMD's
     // other wave (the vector work fills the remaining issue slots).
     __builtin_amdgcn_s_setprio(3);
-    if (g == 1 && i + 5 < n) next_phys = page_of(a, p_lo + i + 5);
+    if (!PRE && g == 1 && i + 5 < n) next_phys = page_of(a, p_lo + i + 5);
     const char *vbase = smem + slot_prev * PP::BUF + v_base;
     const char *kbase = smem + slot_cur * PP::BUF + k_base;
     // operand k: PV (st, dt) = (k / 4, k % 4) for k < 16, QK (ds, mt) = ((k - 16) / 2, k % 2) after
@@ -835,28 +881,43 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
     v8h f[AHEAD];
 #pragma unroll
     for (int k = 0; k < AHEAD; ++k) f[k] = frag(k);
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    S[0] = (v16f)(-m_use);
-    S[1] = (v16f)(-m_use);
+    if constexpr (!PRE) {
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      S[0] = (v16f)(-m_use);
+      S[1] = (v16f)(-m_use);
+    }
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
       if (k < 16) {
         O[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k % AHEAD], pb[k >> 2], O[k & 3], 0, 0, 0);
-        if ((k & 3) == 3) Lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_a, pb[k >> 2], Lacc, 0, 0, 0);
+        if (!PRE && (k & 3) == 3) Lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_a, pb[k >> 2], Lacc, 0, 0, 0);
       } else {
         const int kk = k - 16;
-        S[kk & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k % AHEAD], qf[kk >> 1], S[kk & 1], 0, 0, 0);
+        S[kk & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k % AHEAD], qf[kk >> 1],
+                                                           PRE && kk < 2 ? Minit : S[kk & 1], 0, 0, 0);
       }
       if (k + AHEAD < 32) f[k % AHEAD] = frag(k + AHEAD);
     }
     __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
-      if ((k & 3) == 3 && k < 16)
+      if (!PRE && (k & 3) == 3 && k < 16)
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       else
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (k + AHEAD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (PRE) {
+      // Group 1's pieces of tile i + 1 land before the barrier (all but those
+      // of tile i + 2, issued in its last B phase; vector loads complete in
+      // issue order).
+      if (g == 1) {
+        if (i + 2 < n)
+          wait_older();
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      return;
     }
     // Group 1's DMAs older than its last B phase's (page i + 4 and before)
     // land before the barrier (vector loads complete in issue order); group 0
@@ -904,7 +965,13 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
       const float mnew = fmaxf(m_run, rmx);
       const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mnew);
       m_run = mnew;
-      Lacc[0] *= alpha;
+      if constexpr (PRE) {
+        lsum0 *= alpha;
+        lsum1 *= alpha;
+        Minit = (v16f)(-m_run);
+      } else {
+        Lacc[0] *= alpha;
+      }
 #pragma unroll
       for (int dt = 0; dt < PP::DT; ++dt) O[dt] *= alpha;
       const float delta = m_run == -INFINITY ? 0.f : m_run - m_use;
@@ -916,14 +983,36 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pb[2 * mt + (j >> 1)][4 * (j & 1) + e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(S[mt][4 * j + e]));
+        for (int e = 0; e < 4; ++e) {
+          const float pr = __builtin_amdgcn_exp2f(S[mt][4 * j + e]);
+          if constexpr (PRE) {
+            if (e & 1)
+              lsum1 += pr;
+            else
+              lsum0 += pr;
+          }
+          pb[2 * mt + (j >> 1)][4 * (j & 1) + e] = static_cast<_Float16>(pr);
+        }
   };
 
   // B(i): this group's half of tile i + 1 + g from the fetched inputs, group
   // 1's DMAs of page i + 5 (four per wave, three in the fourth), then softmax(i).
   auto phase_b = [&](int i) {
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (PRE) {
+      // Softmax, then this wave's pieces of tile i + 3 (group 1) or i + 2
+      // (group 0); group 0 then waits for its pieces of tile i + 1.
+      if (i >= 0 && i < n) softmax(i);
+      const int q = i + 2 + g;
+      if (q < n) tile_dma(q);
+      if (g == 0) {
+        if (q < n)
+          wait_older();
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      return;
+    }
     const int ct = i + 1 + g;
     if (ct < n) {
       char *buf = smem + (ct % 3) * PP::BUF;
@@ -936,14 +1025,17 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
 
   // Group 1 starts half a page late: its B(-1) converts and stages only.
   if (g == 1) {
-    if (n > 4) next_phys = page_of(a, p_lo + 4);
+    if (!PRE && n > 4) next_phys = page_of(a, p_lo + 4);
     phase_b(-1);
     lds_barrier();
   }
   // slot = i % 3 for page i; slot_m1 = (i - 1) % 3.
   int slot = 0, slot_m1 = 2;
   for (int i = 0; i <= n; ++i) {
-    phase_a(i, slot_m1, slot);
+    if constexpr (PRE)
+      phase_a(i, (i - 1) & 3, i & 3);
+    else
+      phase_a(i, slot_m1, slot);
     lds_barrier();
     // Group 1's B(n) would be empty; skipping it keeps both groups at 2n + 2 barriers.
     if (g == 0 || i < n) {
@@ -957,7 +1049,11 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
   __builtin_amdgcn_s_setprio(0);
   // ---- finalize: O = 16 acc / l (row sums from lane r32's Lacc[0]; V^T holds V / 16).
   float l;
-  {
+  if constexpr (PRE) {
+    l = lsum0 + lsum1;
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  } else {
     auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(Lacc[0]), __float_as_uint(Lacc[0]), false, false);
     l = hh == 0 ? Lacc[0] : __uint_as_float(sw[0]);
   }
@@ -993,7 +1089,7 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
     }
 }
 
-template <int D>
+template <int D, bool PRE>
 __global__ __attribute__((amdgpu_flat_work_group_size(Tile<D>::THREADS, Tile<D>::THREADS),
                           amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
 prefill_kernel(PrefillArgs a) {
@@ -1009,26 +1105,69 @@ prefill_kernel(PrefillArgs a) {
   const int lane = tid % 64;
   if constexpr (D == 128) {
     // The ping-pong ring starts zeroed: its tiles then only ever hold finite values.
-    for (int o = 16 * tid; o < PP::STAGE_OFF; o += 16 * PP::THREADS) *reinterpret_cast<uint4 *>(smem + o) = make_uint4(0, 0, 0, 0);
+    for (int o = 16 * tid; o < 4 * PP::BUF; o += 16 * PP::THREADS) *reinterpret_cast<uint4 *>(smem + o) = make_uint4(0, 0, 0, 0);
   }
   int s = s0;
   bool first = true;
   while (s < s1) {
-    const int h = s / a.tper;
+    const int hl = s / a.tper;
+    const int h = a.head0 + hl;
     int rb, before;
-    locate_block(a, s - h * a.tper, lane, rb, before);
+    locate_block(a, s - hl * a.tper, lane, rb, before);
     const int n = block_pages(a, rb);
-    const int p_lo = s - h * a.tper - before;
+    const int p_lo = s - hl * a.tper - before;
     const int p_hi = min(n, p_lo + (s1 - s));
     float *part = nullptr;
     if (p_lo != 0 || p_hi != n)
       part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * T::ROWS * (D + 2);
     if constexpr (D == 128)
-      run_segment_pp(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+      run_segment_pp<PRE>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     else
       run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     s += p_hi - p_lo;
     first = false;
+  }
+}
+
+// Dequantizes every page of KV head h once into its tile image (the LDS
+// layout of run_segment_pp's ring): one work-group of 256 threads per page,
+// two K chunks and two V items per thread, the same arithmetic as the
+// in-kernel conversion.
+__global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, char *tiles, int h) {
+  constexpr int D = PP::D;
+  const int p = blockIdx.x;
+  const int64_t phys = page_of(a, p);
+  char *buf = tiles + static_cast<int64_t>(p) * PP::BUF;
+  const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + h * D;
+  const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps + h * (D / 2);
+  const char *ksb = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + h * 4;
+  const char *vsb = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + h * 4;
+  const char *vzb = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + h * 4;
+  const int64_t krow = static_cast<int64_t>(a.hkv) * D, vrow = static_cast<int64_t>(a.hkv) * (D / 2);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + 256 * r;
+    const int key = c >> 3, part = c & 7;
+    PPKIn in;
+    in.k = *reinterpret_cast<const uint4 *>(kb + key * krow + 16 * part);
+    in.ks = *reinterpret_cast<const float *>(ksb + static_cast<int64_t>(key) * a.hkv * 4);
+    pp_emit_k(a, p, in, buf, key * PP::KROW + 32 * part, key);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const PPLane L = pp_lane(a, threadIdx.x, 0, r, 0);
+    const int pair = threadIdx.x & 31, sub = (threadIdx.x >> 5) & 1, hv = (threadIdx.x >> 6) & 1;
+    const int q = 2 * r + (threadIdx.x >> 7);
+    const int k0 = 2 * pair;
+    const int off = 16 * q + 8 * hv + 4 * sub;
+    PPVIn in;
+    in.ev = *reinterpret_cast<const uint32_t *>(vb + k0 * vrow + off);
+    in.od = *reinterpret_cast<const uint32_t *>(vb + (k0 + 1) * vrow + off);
+    in.vs = make_float2(*reinterpret_cast<const float *>(vsb + static_cast<int64_t>(k0) * a.hkv * 4),
+                        *reinterpret_cast<const float *>(vsb + static_cast<int64_t>(k0 + 1) * a.hkv * 4));
+    in.vz = make_float2(*reinterpret_cast<const float *>(vzb + static_cast<int64_t>(k0) * a.hkv * 4),
+                        *reinterpret_cast<const float *>(vzb + static_cast<int64_t>(k0 + 1) * a.hkv * 4));
+    pp_emit_v(a, p, in, buf, L);
   }
 }
 
@@ -1038,7 +1177,8 @@ template <int D>
 __global__ __launch_bounds__(2 * Tile<D>::ROWS) void prefill_merge_kernel(PrefillArgs a) {
   constexpr int R = Tile<D>::ROWS;
   const int b = blockIdx.x;
-  const int h = b / a.nbh, rb = b % a.nbh;
+  const int hl = b / a.nbh, rb = b % a.nbh;
+  const int h = a.head0 + hl;
   const int lane = threadIdx.x % 64;
   int start = 0;
   {
@@ -1051,7 +1191,7 @@ __global__ __launch_bounds__(2 * Tile<D>::ROWS) void prefill_merge_kernel(Prefil
       for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
       base += n;
     }
-    start = h * a.tper + base;
+    start = hl * a.tper + base;
   }
   const int n = block_pages(a, rb);
   const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
@@ -1123,6 +1263,20 @@ int64_t partial_bytes(int grid, int head_dim) {
   return static_cast<int64_t>(grid) * 2 * rows_per_block(head_dim) * (head_dim + 2) * 4;
 }
 
+// Head dim 128 dequantizes each page once per KV head into the workspace when
+// that work is shared by at least this many row blocks (below it the
+// in-kernel conversion costs less than the extra tile traffic).
+constexpr int kPreMinBlocks = 4;
+
+bool use_tiles(const PrefillPlan &pl, int head_dim) { return head_dim == 128 && pl.nbh >= kPreMinBlocks; }
+
+// Workspace: partial states, then (tiles) one head's tile images, 256-byte aligned.
+int64_t tiles_offset(const PrefillPlan &pl, int head_dim) { return (partial_bytes(pl.grid, head_dim) + 255) / 256 * 256; }
+int64_t workspace_need(const PrefillPlan &pl, int64_t seq_len, int head_dim) {
+  if (!use_tiles(pl, head_dim)) return partial_bytes(pl.grid, head_dim);
+  return tiles_offset(pl, head_dim) + (seq_len + kPage - 1) / kPage * PP::BUF;
+}
+
 }  // namespace
 }  // namespace k8v4
 
@@ -1132,7 +1286,7 @@ extern "C" int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, 
   if (q_len == 0) return 0;
   PrefillPlan pl;
   if (!plan_prefill(seq_len, q_len, hkv, head_dim, pl)) return -1;
-  return partial_bytes(pl.grid, head_dim);
+  return workspace_need(pl, seq_len, head_dim);
 }
 
 extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
@@ -1203,7 +1357,7 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   PrefillPlan pl;
   K8V4_REQUIRE(plan_prefill(seq_len, q_len, hkv, head_dim, pl), "prefill too large for one call (q_len %lld, seq_len %lld)",
                static_cast<long long>(q_len), static_cast<long long>(seq_len));
-  const int64_t need = partial_bytes(pl.grid, head_dim);
+  const int64_t need = workspace_need(pl, seq_len, head_dim);
   K8V4_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                "prefill workspace must be a 16-byte aligned device buffer");
   if (workspace_bytes < need) {
@@ -1218,11 +1372,33 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   a.grid = pl.grid;
   a.xcd_perm = pl.grid % 8 == 0 ? 1 : 0;
   a.ws = static_cast<float *>(workspace);
+  a.head0 = 0;
+  a.tiles = nullptr;
   auto s = static_cast<hipStream_t>(stream);
+  if (use_tiles(pl, head_dim)) {
+    // One KV head at a time: its pages dequantized once into the workspace,
+    // then all row blocks of the head over them, then their merge.
+    char *tiles = static_cast<char *>(workspace) + tiles_offset(pl, head_dim);
+    const unsigned npages = static_cast<unsigned>((seq_len + kPage - 1) / kPage);
+    a.total = pl.tper;
+    a.grid = std::min(pl.tper, device_cus());
+    if (a.grid >= 8) a.grid -= a.grid % 8;
+    a.xcd_perm = a.grid % 8 == 0 ? 1 : 0;
+    a.tiles = tiles;
+    for (int h = 0; h < hkv; ++h) {
+      a.head0 = h;
+      prefill_convert_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
+      prefill_kernel<128, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(PP::THREADS), 0, s>>>(a);
+      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh)), dim3(2 * Tile<128>::ROWS), 0, s>>>(a);
+      const int rc = launch_status("k8v4_prefill_paged");
+      if (rc) return rc;
+    }
+    return K8V4_OK;
+  }
   if (head_dim == 128)
-    prefill_kernel<128><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<128>::THREADS), 0, s>>>(a);
+    prefill_kernel<128, false><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<128>::THREADS), 0, s>>>(a);
   else
-    prefill_kernel<256><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<256>::THREADS), 0, s>>>(a);
+    prefill_kernel<256, false><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<256>::THREADS), 0, s>>>(a);
   const int rc = launch_status("k8v4_prefill_paged");
   if (rc) return rc;
   const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv));

@@ -171,18 +171,19 @@ def test_prefill_blocks_split_across_many_work_groups(gpu_ops, q_len, seq_len):
     assert gpu_ops.prefill_workspace_bytes(seq_len, q_len, 4, 128) > 0
 
 
-@pytest.mark.parametrize("d", [128, 256])
-def test_prefill_values_near_the_fp16_limit(gpu_ops, d):
+@pytest.mark.parametrize("d,q_len", [(128, 40), (128, 200), (256, 40)])
+def test_prefill_values_near_the_fp16_limit(gpu_ops, d, q_len):
     """Every 7th token's V row alternates 60000 / -65504 (its -65504 codes
     dequantize to -8 * 125504 / 15 = -66935, beyond fp16) and its K row draws
     almost all of the softmax weight, so outputs exceed 65504 in magnitude:
     the dequantized tiles and the accumulation must stay finite and match the
-    oracle for fp32 output."""
-    print("prefill large V d=%d" % d, flush=True)
+    oracle for fp32 output (200 query tokens take the path that dequantizes
+    each page once per head, 40 the in-kernel conversion)."""
+    print("prefill large V d=%d q_len=%d" % (d, q_len), flush=True)
     lay = PageLayout(2, d)
     cache = Cache(64, lay)
     gen = torch.Generator().manual_seed(43)
-    L, q_len = 3000, 40
+    L = 3000
     table = random_tables(gen, [L], 64)
     t = torch.arange(L)
     slots = (table[0].long()[t // PAGE] * PAGE + t % PAGE).to(DEV)
