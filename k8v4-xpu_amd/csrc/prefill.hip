@@ -865,9 +865,11 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
   // (the ring starts zeroed) by a zero operand, and QK(n) fills scores that
   // are never read.  Then the inputs of the next conversion are read.
   auto phase_a = [&](int i, int slot_prev, int slot_cur) {
-    // The wave feeding the matrix core wins issue conflicts with its SIMD's
-    // other wave (the vector work fills the remaining issue slots).
-    __builtin_amdgcn_s_setprio(3);
+    // With the dequantization in the vector phase, the wave feeding the matrix
+    // core wins issue conflicts with its SIMD's other wave (the vector work
+    // fills the remaining issue slots); with pre-converted tiles the vector
+    // phase is short and equal priority measures faster.
+    if constexpr (!PRE) __builtin_amdgcn_s_setprio(3);
     if (!PRE && g == 1 && i + 5 < n) next_phys = page_of(a, p_lo + i + 5);
     const char *vbase = smem + slot_prev * PP::BUF + v_base;
     const char *kbase = smem + slot_cur * PP::BUF + k_base;
@@ -877,7 +879,7 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
       const int kk = k - 16;
       return *reinterpret_cast<const v8h *>(kbase + 32 * (kk & 1) * PP::KROW + 32 * (kk >> 1));
     };
-    constexpr int AHEAD = 8;
+    constexpr int AHEAD = PRE ? 12 : 8;  // operand reads in flight (register budget)
     v8h f[AHEAD];
 #pragma unroll
     for (int k = 0; k < AHEAD; ++k) f[k] = frag(k);
