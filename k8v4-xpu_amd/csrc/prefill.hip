@@ -1132,53 +1132,60 @@ prefill_kernel(PrefillArgs a) {
 }
 
 // Dequantizes every page of KV head h once into its tile image (the LDS
-// layout of run_segment_pp's ring): one work-group of 256 threads per page,
-// two K chunks and two V items per thread, the same arithmetic as the
-// in-kernel conversion.
+// layout of run_segment_pp's ring): one work-group of 256 threads per page.
+// The page's V codes and scale planes are staged in LDS with coalesced loads
+// in the order the in-kernel conversion stages them; then each thread
+// dequantizes two K chunks (read directly) and two V items with the same
+// arithmetic as the in-kernel conversion.
 __global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, char *tiles, int h) {
   constexpr int D = PP::D;
-  const int p = blockIdx.x;
+  __shared__ __attribute__((aligned(16))) char st[PP::STAGE];
+  const int p = blockIdx.x, t = threadIdx.x;
   const int64_t phys = page_of(a, p);
   char *buf = tiles + static_cast<int64_t>(p) * PP::BUF;
   const char *kb = reinterpret_cast<const char *>(a.k_cache) + phys * a.k_ps + h * D;
   const char *vb = reinterpret_cast<const char *>(a.v_cache) + phys * a.v_ps + h * (D / 2);
-  const char *ksb = reinterpret_cast<const char *>(a.k_scale) + phys * a.ks_ps + h * 4;
-  const char *vsb = reinterpret_cast<const char *>(a.v_scale) + phys * a.vs_ps + h * 4;
-  const char *vzb = reinterpret_cast<const char *>(a.v_zero) + phys * a.vz_ps + h * 4;
   const int64_t krow = static_cast<int64_t>(a.hkv) * D, vrow = static_cast<int64_t>(a.hkv) * (D / 2);
+  {
+    // V piece q (16 bytes) of key 2 * pair + parity -> [q][parity][pair]
+    const int key = t >> 2, q = t & 3;
+    *reinterpret_cast<uint4 *>(st + PP::SV_OFF + (q * 64 + (key & 1) * 32 + (key >> 1)) * 16) =
+        *reinterpret_cast<const uint4 *>(vb + key * vrow + 16 * q);
+    if (t < 192) {
+      const int plane = t >> 6, k = t & 63;
+      const float *src = plane == 0 ? a.k_scale : plane == 1 ? a.v_scale : a.v_zero;
+      const int64_t ps = plane == 0 ? a.ks_ps : plane == 1 ? a.vs_ps : a.vz_ps;
+      reinterpret_cast<float *>(st + PP::SS_OFF)[t] =
+          *reinterpret_cast<const float *>(reinterpret_cast<const char *>(src) + phys * ps + (static_cast<int64_t>(k) * a.hkv + h) * 4);
+    }
+  }
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int c = threadIdx.x + 256 * r;
+    const int c = t + 256 * r;
     const int key = c >> 3, part = c & 7;
     PPKIn in;
     in.k = *reinterpret_cast<const uint4 *>(kb + key * krow + 16 * part);
-    in.ks = *reinterpret_cast<const float *>(ksb + static_cast<int64_t>(key) * a.hkv * 4);
+    in.ks = reinterpret_cast<const float *>(st + PP::SS_OFF)[key];
     pp_emit_k(a, p, in, buf, key * PP::KROW + 32 * part, key);
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const PPLane L = pp_lane(a, threadIdx.x, 0, r, 0);
-    const int pair = threadIdx.x & 31, sub = (threadIdx.x >> 5) & 1, hv = (threadIdx.x >> 6) & 1;
-    const int q = 2 * r + (threadIdx.x >> 7);
-    const int k0 = 2 * pair;
-    const int off = 16 * q + 8 * hv + 4 * sub;
-    PPVIn in;
-    in.ev = *reinterpret_cast<const uint32_t *>(vb + k0 * vrow + off);
-    in.od = *reinterpret_cast<const uint32_t *>(vb + (k0 + 1) * vrow + off);
-    in.vs = make_float2(*reinterpret_cast<const float *>(vsb + static_cast<int64_t>(k0) * a.hkv * 4),
-                        *reinterpret_cast<const float *>(vsb + static_cast<int64_t>(k0 + 1) * a.hkv * 4));
-    in.vz = make_float2(*reinterpret_cast<const float *>(vzb + static_cast<int64_t>(k0) * a.hkv * 4),
-                        *reinterpret_cast<const float *>(vzb + static_cast<int64_t>(k0 + 1) * a.hkv * 4));
-    pp_emit_v(a, p, in, buf, L);
+    const PPLane L = pp_lane(a, t, 0, r, 0);
+    pp_emit_v(a, p, pp_fetch_v(st, L), buf, L);
   }
 }
 
-// Finishes the blocks split between work-groups: one work-group per block,
-// two threads per row, D/2 dims each.
+// Finishes the blocks split between work-groups: kMergeSplit work-groups per
+// block (a quarter of its rows each, so a launch fills the chip), two threads
+// per row, D/2 dims each.
+constexpr int kMergeSplit = 4;
+
 template <int D>
-__global__ __launch_bounds__(2 * Tile<D>::ROWS) void prefill_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_merge_kernel(PrefillArgs a) {
   constexpr int R = Tile<D>::ROWS;
-  const int b = blockIdx.x;
+  const int b = blockIdx.x / kMergeSplit;
+  const int quarter = blockIdx.x % kMergeSplit;
   const int hl = b / a.nbh, rb = b % a.nbh;
   const int h = a.head0 + hl;
   const int lane = threadIdx.x % 64;
@@ -1198,7 +1205,7 @@ __global__ __launch_bounds__(2 * Tile<D>::ROWS) void prefill_merge_kernel(Prefil
   const int n = block_pages(a, rb);
   const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
   if (va == vb) return;  // one work-group did the whole block
-  const int lr = threadIdx.x / 2, half = threadIdx.x % 2;
+  const int lr = quarter * (R / kMergeSplit) + threadIdx.x / 2, half = threadIdx.x % 2;
   const int row = rb * R + lr;
   if (row >= a.q_len * 6) return;
   float M = -INFINITY;
@@ -1391,7 +1398,7 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
       a.head0 = h;
       prefill_convert_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
       prefill_kernel<128, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(PP::THREADS), 0, s>>>(a);
-      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh)), dim3(2 * Tile<128>::ROWS), 0, s>>>(a);
+      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(a);
       const int rc = launch_status("k8v4_prefill_paged");
       if (rc) return rc;
     }
@@ -1403,10 +1410,10 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
     prefill_kernel<256, false><<<dim3(static_cast<unsigned>(pl.grid)), dim3(Tile<256>::THREADS), 0, s>>>(a);
   const int rc = launch_status("k8v4_prefill_paged");
   if (rc) return rc;
-  const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv));
+  const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv * kMergeSplit));
   if (head_dim == 128)
-    prefill_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS), 0, s>>>(a);
+    prefill_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(a);
   else
-    prefill_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS), 0, s>>>(a);
+    prefill_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS / kMergeSplit), 0, s>>>(a);
   return launch_status("k8v4_prefill_paged merge");
 }
