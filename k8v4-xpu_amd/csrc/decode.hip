@@ -733,7 +733,13 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
     lmx[nt] = mx;
     // A row's largest score passes the threshold exactly when one of its four
     // lanes' does, so the cross-lane max is only taken on a rescale.
-    grow |= mx > st.thr[nt];
+    // (D = 256 compares in the scaled domain instead of keeping the
+    // thresholds: three fewer registers where the output accumulators take
+    // nearly all of them.)
+    if constexpr (D == 256)
+      grow |= mx * st.crow[nt] > st.m_run[nt] + kRescaleThreshold;
+    else
+      grow |= mx > st.thr[nt];
   }
   if (__ballot(grow)) {
 #pragma unroll
@@ -742,16 +748,23 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
       const float alpha = st.m_run[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m_run[nt] - mnew);
       st.m_run[nt] = mnew;
       st.thr[nt] = (mnew + kRescaleThreshold) / st.crow[nt];
+      float ai[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ai = __shfl(alpha, 4 * g + i, kWave);
-        st.lsum[nt][i] *= ai;
-        st.corr[nt][i] *= ai;
-#pragma unroll
-        for (int dg = 0; dg < DG; ++dg)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) st.O[nt][dg][j][i] *= ai;
+        ai[i] = __shfl(alpha, 4 * g + i, kWave);
+        st.lsum[nt][i] *= ai[i];
+        st.corr[nt][i] *= ai[i];
       }
+      // One 16 x 16 accumulator tile at a time (a fence between tiles keeps
+      // the compiler from moving every accumulator through registers at once).
+#pragma unroll
+      for (int dg = 0; dg < DG; ++dg)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st.O[nt][dg][j][i] *= ai[i];
+          if constexpr (D == 256) __builtin_amdgcn_sched_barrier(0);
+        }
     }
   }
   // ---- P = exp2(score * c - m), packed fp16 in the PV A-operand layout; row sums by MFMA
@@ -1207,7 +1220,10 @@ void decode_split_kernel(DecodeArgs a) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
+      int lane_o = lane;
+      asm volatile("" : "+v"(lane_o));
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1219,7 +1235,10 @@ void decode_split_kernel(DecodeArgs a) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
+      int lane_o = lane;
+      asm volatile("" : "+v"(lane_o));
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1229,7 +1248,10 @@ void decode_split_kernel(DecodeArgs a) {
     if (k + RV < cnt) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RV) * NWH;
-      issue_v<D, HKV>(a, page_of(xr), xr, lo, lane, vslot);
+      int lane_o = lane;
+      asm volatile("" : "+v"(lane_o));
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
+      issue_v<D, HKV>(a, page_of(xr), xr, lo_r, lane, vslot);
       issued += S::NVS;
 #pragma unroll
       for (int s = 0; s < RV; ++s)
