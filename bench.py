@@ -538,7 +538,7 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
             "TFLOPs": round(tflops, 1),
             "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
             "mfma_utilization": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "dtype": "f16 MFMA (K tile fp16 code x scale, exact V nibbles), f32 accumulation",
+            "dtype": "f16 MFMA (fp16 tiles: K code x k_scale, V (nibble - v_zero) x v_scale / 16), f32 accumulation",
         }
         del w
         torch.cuda.empty_cache()
