@@ -94,6 +94,7 @@ struct DecodeArgs {
   int grid;              // number of split work-groups (the plan's G)
   int min_pages;
   int merge_cs;   // column slices per output row in the merge
+  int tile0;      // first 16-row query tile of this split launch (D = 256, four tiles: two launches of two)
   int units;      // merge units: output rows x merge_cs
   void *out;
   int out_dtype;
@@ -674,7 +675,7 @@ __device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const
 template <int D, int NT, bool QLDS>
 __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, const v4i (&sc)[2][NT],
                                                  const lds_t *vslot, int tbase, int L0, int lane, int g,
-                                                 bool masked) {
+                                                 bool masked, const __attribute__((address_space(3))) int *lims) {
   using S = Slot<D>;
   constexpr int DG = S::DG;
   // Phase fences keep the scheduler from hoisting later LDS reads into this
@@ -724,7 +725,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
       for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (tbase + 16 * ml + 4 * g + i >= st.lim[nt]) t[ml][nt][i] = -INFINITY;
+          if (tbase + 16 * ml + 4 * g + i >= (D == 256 ? lims[nt * 16 + (lane & 15)] : st.lim[nt])) t[ml][nt][i] = -INFINITY;
     }
 #pragma unroll
     for (int ml = 0; ml < 2; ++ml)
@@ -868,7 +869,9 @@ struct SplitConfig {
   // up to RK - 1 K slots and RV - 1 V slots are in flight.
   static constexpr int WAVES = HKV * NWH;
   static constexpr int Q_FRAG_BYTES = NT * (D / 64) * kWave * 16;         // int8 B-operand fragments
-  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4;         // + per-row factors
+  // + per-row factors (and at D = 256 the rows' causal ends, kept out of
+  // the registers the 256-dim accumulators fill)
+  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4 * (D == 256 ? 2 : 1);
   // 4 / HKV work-groups share a CU (the grid is about that many per CU).
   static constexpr int LDS_MAX = 163840 * HKV / 4;
   static constexpr bool QLDS =
@@ -932,6 +935,7 @@ void decode_split_kernel(DecodeArgs a) {
   const int x1 = min(2 * p1, (L0 + 31) / 32);
   const int32_t *bt_row = a.block_table + static_cast<int64_t>(b) * a.bt_stride;
   const int rows = a.q_len * kGqa;
+  const int r0 = 16 * a.tile0;  // this launch's tiles are rows r0 .. r0 + 16 NT - 1
 
   // A pre-quantized query tile (k8v4_attn_batch_q8) replaces the raw rows
   // and their quantization below.
@@ -950,7 +954,7 @@ void decode_split_kernel(DecodeArgs a) {
   for (int nt = 0; nt < (QSPLIT ? 0 : NT); ++nt) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = (v4i){0, 0, 0, 0};
-    const int r = 16 * nt + n;
+    const int r = r0 + 16 * nt + n;
     if (r < rows && !pre_q) {
       const int j = r / kGqa;
       const int qh = h * kGqa + (r - j * kGqa);
@@ -979,10 +983,17 @@ void decode_split_kernel(DecodeArgs a) {
       min_end = min(min_end, e);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const int r = 16 * nt + n;
+        const int r = r0 + 16 * nt + n;
         if (r < rows && r / kGqa == j) st.lim[nt] = min(e, L0);
       }
     }
+  }
+  // (D = 256: the causal ends live in LDS after the per-row factors.)
+  const auto *lims = reinterpret_cast<const __attribute__((address_space(3))) int *>(qlds + CFG::Q_FRAG_BYTES) + NT * 16;
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      if (g == 0) const_cast<__attribute__((address_space(3))) int *>(lims)[nt * 16 + n] = st.lim[nt];
   }
 
   // This wave's chunks: x0 + w + k*NWH for k < cnt.
@@ -1057,7 +1068,7 @@ void decode_split_kernel(DecodeArgs a) {
       const int ti = nt / NWH;
 #pragma unroll
       for (int d = 0; d < 16 / RPD; ++d) {
-        const int r = 16 * nt + RPD * d + lane / (2 * D / 16);
+        const int r = r0 + 16 * nt + RPD * d + lane / (2 * D / 16);
         const int rr = r < rows ? r : 0;
         const int j = rr / kGqa;
         const int qh = h * kGqa + (rr - j * kGqa);
@@ -1084,7 +1095,7 @@ void decode_split_kernel(DecodeArgs a) {
       if constexpr (CFG::QLDS) {
         if (nt % NWH != w) continue;
       }
-      const int r = 16 * nt + n;
+      const int r = r0 + 16 * nt + n;
       const bool live = r < rows;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -1108,7 +1119,7 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if (QSPLIT && nt % NWH != w) continue;  // the partner wave quantizes this tile
-      const bool live = 16 * nt + n < rows;
+      const bool live = r0 + 16 * nt + n < rows;
       float x[KS][16];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -1230,7 +1241,7 @@ void decode_split_kernel(DecodeArgs a) {
       for (int s = 0; s < RK; ++s)
         if (sk == s) mk[s] = issued;
     }
-    if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+    if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end, lims);
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1323,7 +1334,7 @@ void decode_split_kernel(DecodeArgs a) {
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * nt + 4 * g + i;
+      const int r = r0 + 16 * nt + 4 * g + i;
       if (r < rows) {
         const float l = st.lsum[nt][i];
         const float f = l > 0.f ? 0.25f / l : 0.f;
@@ -1339,7 +1350,7 @@ void decode_split_kernel(DecodeArgs a) {
         if (n == 0) lbase[h * rows + r] = l;
       }
     }
-    const int r = 16 * nt + n;
+    const int r = r0 + 16 * nt + n;
     if (g == 0 && r < rows) mbase[h * rows + r] = st.m_run[nt];
   }
 }
@@ -1348,13 +1359,26 @@ template <int D, int NT>
 constexpr int waves_per_head() { return (D == 128 && NT <= 3) ? 2 : 1; }
 
 template <int D, int HKV>
-void launch_split(const DecodeArgs &a, int nt, hipStream_t s) {
+void launch_split(DecodeArgs a, int nt, hipStream_t s) {
   const dim3 grid(a.grid);
+  a.tile0 = 0;
+  if (D == 256 && nt == 4) {
+    // Four 256-dim tiles do not fit one wave's registers: two launches of two
+    // tiles each (rows 0-31, then 32-63), writing disjoint rows of the same
+    // split states.
+    decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a);
+    a.tile0 = 2;
+    decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a);
+    return;
+  }
   switch (nt) {
     case 1: decode_split_kernel<D, 1, HKV, waves_per_head<D, 1>()><<<grid, dim3(64 * HKV * waves_per_head<D, 1>()), 0, s>>>(a); break;
     case 2: decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a); break;
     case 3: decode_split_kernel<D, 3, HKV, waves_per_head<D, 3>()><<<grid, dim3(64 * HKV * waves_per_head<D, 3>()), 0, s>>>(a); break;
-    default: decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a); break;
+    default:
+      if constexpr (D == 128)
+        decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a);
+      break;
   }
 }
 

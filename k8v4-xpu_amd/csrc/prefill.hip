@@ -879,7 +879,7 @@ __device__ __forceinline__ void run_segment_pp(const PrefillArgs &a, char *smem,
       const int kk = k - 16;
       return *reinterpret_cast<const v8h *>(kbase + 32 * (kk & 1) * PP::KROW + 32 * (kk >> 1));
     };
-    constexpr int AHEAD = PRE ? 12 : 8;  // operand reads in flight (register budget)
+    constexpr int AHEAD = PRE ? 12 : 6;  // operand reads in flight (register budget)
     v8h f[AHEAD];
 #pragma unroll
     for (int k = 0; k < AHEAD; ++k) f[k] = frag(k);
