@@ -113,7 +113,10 @@ int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_tok_stride, i
  *      seq_len - q_len + j + 1.  A row with no visible key outputs zeros.
  * out: [batch*q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride.
  * workspace: caller-owned device scratch (16-byte aligned) of
- *      workspace_bytes; k8v4_attn_workspace_bytes() gives what a call needs.
+ *      workspace_bytes; k8v4_attn_workspace_bytes() gives what a call needs:
+ *      the split states and, for head_dim 256 with hkv 2, ahead of them the
+ *      query quantized by a first kernel (per sequence and KV head 64 rows of
+ *      256 int8 codes, then the rows' fp32 scales).
  * num_splits: split-K work-groups (0 = about one per CU).
  * Requires 1 <= q_len and q_len*6 <= 64.
  */

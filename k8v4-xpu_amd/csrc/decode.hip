@@ -31,6 +31,13 @@
 //    P.V and the row sums on v_mfma_f32_16x16x32_f16 with fp32 accumulation.
 //  * Each split writes (m, l, O / l in fp16) for its live rows only; a small
 //    merge kernel combines the splits of each output row.
+//  * Head dim 256 with two KV heads runs as paired halves: the cache's rows
+//    are read as those of a 128-dim cache with four heads, two waves per
+//    SIMD; the two waves of a pair score each chunk over both of their K
+//    slots and each accumulates its own 128 output dims (a 256-dim wave needs
+//    all 512 registers of a SIMD lane, so one wave per SIMD, latency-bound).
+//    Its query is quantized by a small kernel ahead of the split kernel, once
+//    for all work-groups.
 #include "k8v4_common.h"
 
 #include <cfloat>
@@ -493,6 +500,23 @@ __device__ __forceinline__ void dma4s(const void *sbase, uint32_t voff, const ld
                : "memory", "m0");
 }
 
+// Split-state stores at device scope (sc1): written through the XCD's L2 to
+// memory, where the merge kernel reads them.  With default stores the states
+// of the work-groups that finish last are still dirty in L2 when the kernel
+// ends, and the end-of-kernel write-back of them delays the merge launch
+// (4 x 8,192 tokens, q = 7: 1.5 us per step).  Vector stores; they are the
+// last memory operations of the kernel, so the compiler's wait counting, which
+// does not see them, has nothing after them to order.  Its hazard checks do
+// not see them either: a store of more than 8 bytes still reads its data
+// registers after issue, so the statement itself waits the states before a
+// later instruction may overwrite them (s_nop 1).
+__device__ __forceinline__ void store_wt16(void *dst, v8h v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_wt4(float *dst, float v) {
+  asm volatile("global_store_dword %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
+}
+
 // Per-lane byte offsets of one chunk's DMA sources (loop-invariant).
 struct LaneOffsets {
   uint32_t k[4];  // K source per DMA index mod 4: row L/(D/16) of the piece, swizzled chunk
@@ -504,9 +528,12 @@ struct LaneOffsets {
   uint32_t sa, sb;
 };
 
-template <int D, int HKV>
+// PH (paired halves, head dim 256 served as two 128-dim halves): h and HKV
+// count half-heads; the scale planes belong to the whole head h / 2 of HKV / 2.
+template <int D, int HKV, bool PH = false>
 __device__ __forceinline__ LaneOffsets lane_offsets(const DecodeArgs &a, int h, int lane) {
   constexpr int VROW = D / 2, KRP = 1024 / D, CPR = D / 16;
+  constexpr int HS = PH ? HKV / 2 : HKV;  // heads of the scale planes
   LaneOffsets o;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -522,7 +549,7 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const DecodeArgs &a, int h, 
     const int row = VROW == 64 ? 4 * (pos >> 2) + (((pos & 3) - (pos >> 2)) & 3) : pos;
     o.v = static_cast<uint32_t>(row * (HKV * VROW) + h * VROW + (lane * 16) % VROW);
   }
-  o.s = static_cast<uint32_t>(((lane & 31) * HKV + h) * 4);
+  o.s = static_cast<uint32_t>(((lane & 31) * HS + (PH ? h >> 1 : h)) * 4);
   const int64_t lo_kv = a.d_kv < 0 ? a.d_kv : 0, lo_vz = a.d_vz < 0 ? a.d_vz : 0;
   o.sa = o.s + static_cast<uint32_t>(lane < 32 ? -lo_kv : a.d_kv - lo_kv);
   o.sb = o.s + static_cast<uint32_t>(lane < 32 ? -lo_vz : a.d_vz - lo_vz);
@@ -549,10 +576,11 @@ __device__ __forceinline__ int issue_k(const DecodeArgs &a, int phys, int x, con
   return valid;
 }
 
-template <int D, int HKV>
+template <int D, int HKV, bool PH = false>
 __device__ __forceinline__ void issue_v(const DecodeArgs &a, int phys, int x, const LaneOffsets &lo, int lane,
                                         lds_t *vslot) {
   using S = Slot<D>;
+  constexpr int HS = PH ? HKV / 2 : HKV;  // heads of the scale planes
   const int half = x & 1;
   if (phys < 0) phys = 0;
   const int tok0 = 32 * half;
@@ -563,7 +591,7 @@ __device__ __forceinline__ void issue_v(const DecodeArgs &a, int phys, int x, co
   // Two full-wave 4-byte DMAs, no divergent branch: ks[32] | vs[32] at
   // S_OFF, then vs[32] | vz[32] at S_OFF + 128 (the v_scale cells are written
   // twice with the same values).
-  const int64_t plane0 = static_cast<int64_t>(tok0) * HKV * 4;
+  const int64_t plane0 = static_cast<int64_t>(tok0) * HS * 4;
   if (a.planes_fast) {
     const int64_t lo_kv = a.d_kv < 0 ? a.d_kv : 0, lo_vz = a.d_vz < 0 ? a.d_vz : 0;
     const char *pa = reinterpret_cast<const char *>(a.k_scale) + lo_kv + phys * a.ks_ps + plane0;
@@ -668,6 +696,63 @@ __device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const
 #pragma unroll
       for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
     }
+}
+
+// QK^T of a 256-dim head from two 128-dim K slots (paired halves): dims
+// 0-127 of the chunk's keys in `klo`, dims 128-255 in `khi` (the slots of the
+// two waves of the pair), the query fragments of all four 64-dim k-steps in
+// LDS.  Same score layout and bias as chunk_qk; |dot| <= 256 * 127 * 127 <
+// 2^22 keeps the biased accumulator exact.  The two halves' K operands are
+// read one half at a time (16 registers instead of 32).
+template <int NT>
+__device__ __forceinline__ void chunk_qk_pair(const lds_t *klo, const lds_t *khi, const lds_t *qlds, int lane, int g,
+                                              v4i (&sc)[2][NT]) {
+  const int n = lane & 15;
+#pragma unroll
+  for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) sc[ml][nt] = (v4i){kScoreBias, kScoreBias, kScoreBias, kScoreBias};
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const lds_t *kslot = part ? khi : klo;
+    v4i kf[2][2];
+#pragma unroll
+    for (int ml = 0; ml < 2; ++ml)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int t = 16 * ml + n, c = 4 * ks + g;
+        kf[ml][ks] = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
+            kslot + t * 128 + 16 * (c ^ kswz<128>(t)));
+      }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const v4i qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
+            qlds + ((nt * 4 + 2 * part + ks) * kWave + lane) * 16);
+#pragma unroll
+        for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Flags of the paired-halves handshake, one word per wave in LDS.  A flag
+// only grows within a launch; a wait polls its partner's word (wave-uniform)
+// until it reaches the target, sleeping between polls.  The pair runs the
+// same chunk sequence and neither wave waits before publishing what the
+// other waits for, so every wait ends; the bound only caps a wait that a
+// broken launch could otherwise make endless.
+typedef __attribute__((address_space(3))) int lds_int;
+__device__ __forceinline__ void pair_flag_set(lds_int *f, int v, int lane) {
+  if (lane == 0) *reinterpret_cast<volatile lds_int *>(f) = v;
+}
+__device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target) {
+  for (int it = 0; it < (1 << 22); ++it) {
+    const int v = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const volatile lds_int *>(f));
+    if (v >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
 }
 
 // Softmax and P.V of one chunk whose scores chunk_qk produced; reads the V
@@ -857,7 +942,7 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
       }
 }
 
-template <int D, int NT, int HKV, int NWH>
+template <int D, int NT, int HKV, int NWH, bool PH = false>
 struct SplitConfig {
   // The int8 Q operands live in LDS with two waves per head (shared by the
   // pair) and with one wave per head at D = 256 when a two-slot K ring still
@@ -867,30 +952,39 @@ struct SplitConfig {
   // deep as the LDS allows; with two waves per SIMD a K slot is refilled as
   // soon as its QK^T product is issued, so while a wave computes one chunk
   // up to RK - 1 K slots and RV - 1 V slots are in flight.
+  // Paired halves (PH): D = 128 and HKV half-heads serve a 256-dim cache of
+  // HKV / 2 heads; the query fragments (all 256 dims) are kept per whole head.
+  static constexpr int DQ = PH ? 2 * D : D;       // dims of one score
+  static constexpr int QHEADS = PH ? HKV / 2 : HKV;
   static constexpr int WAVES = HKV * NWH;
-  static constexpr int Q_FRAG_BYTES = NT * (D / 64) * kWave * 16;         // int8 B-operand fragments
+  static constexpr int Q_FRAG_BYTES = NT * (DQ / 64) * kWave * 16;        // int8 B-operand fragments
   // + per-row factors (and at D = 256 the rows' causal ends, kept out of
   // the registers the 256-dim accumulators fill)
   static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4 * (D == 256 ? 2 : 1);
   // 4 / HKV work-groups share a CU (the grid is about that many per CU).
   static constexpr int LDS_MAX = 163840 * HKV / 4;
   static constexpr bool QLDS =
-      NWH > 1 || (D == 256 && HKV * Q_LDS_BYTES + WAVES * (2 * Slot<D>::K_BYTES + 2 * Slot<D>::V_BYTES) <= LDS_MAX);
+      PH || NWH > 1 || (D == 256 && HKV * Q_LDS_BYTES + WAVES * (2 * Slot<D>::K_BYTES + 2 * Slot<D>::V_BYTES) <= LDS_MAX);
   static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_LDS_BYTES : 0;
-  static constexpr int Q_TOTAL = HKV * Q_BYTES_PER_HEAD;
+  static constexpr int Q_TOTAL = QHEADS * Q_BYTES_PER_HEAD;
+  // PH handshake words: per wave, the chunks whose K half is resident and
+  // the chunks whose K slots it has finished reading.
+  static constexpr int FLAG_BYTES = PH ? 2 * WAVES * 4 : 0;
   // One wave per SIMD (NWH == 1) has no partner wave to cover the table
   // lookup of a mid-chunk refill: it refills its K slot after P.V, next to
-  // the V slot.
-  static constexpr bool K_EARLY = NWH > 1;
+  // the V slot.  So does a PH wave, whose slot the other half of its pair
+  // reads during its own QK^T.
+  static constexpr bool K_EARLY = NWH > 1 && !PH;
   static constexpr int RV = 2;
-  static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
+  static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL - FLAG_BYTES) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
   static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
   static constexpr int WAVE_BYTES = RK * Slot<D>::K_BYTES + RV * Slot<D>::V_BYTES;
   // Loads issued after a chunk's V group until that chunk is consumed, in
   // the steady state of the main loop (one K and one V group per chunk).
   static constexpr int STEADY_AFTER = (RV - 1) * (Slot<D>::NK + Slot<D>::NVS);
   static constexpr int Q_OFF = WAVES * WAVE_BYTES;
-  static constexpr int RING_BYTES = Q_OFF + HKV * Q_BYTES_PER_HEAD;
+  static constexpr int FLAG_OFF = Q_OFF + Q_TOTAL;
+  static constexpr int RING_BYTES = FLAG_OFF + FLAG_BYTES;
   // Partner-wave state exchange at the end (reuses the ring memory).
   static constexpr int XCHG_FLOATS = (NT * (D / 128) * 8 * 4 + NT * 4 + NT) * kWave;
   static constexpr int XCHG_BYTES = NWH > 1 ? HKV * XCHG_FLOATS * 4 : 0;
@@ -903,12 +997,22 @@ struct SplitConfig {
                 "query staging does not fit the K ring");
 };
 
-template <int D, int NT, int HKV, int NWH>
+// PH: paired halves.  A 256-dim cache of HKV / 2 heads is served as HKV
+// 128-dim half-heads (its K rows [token][HKV/2][256] and V rows
+// [token][HKV/2][128 B] are exactly the rows of a 128-dim cache of HKV
+// heads): waves h = 2 hh + half load and compute on dims 128 half .. + 127 of
+// head hh; the two waves of a pair build each chunk's 256-dim scores from
+// both of their K slots (an LDS handshake per chunk orders the slot reads
+// against the DMAs), run the same softmax and accumulate P.V over their own
+// 128 output dims.  The query comes pre-quantized (256-dim rows, one scale
+// per row).
+template <int D, int NT, int HKV, int NWH, bool PH = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV * NWH, 64 * HKV * NWH),
                           amdgpu_waves_per_eu(NWH, NWH)))
 void decode_split_kernel(DecodeArgs a) {
+  static_assert(!PH || D == 128, "paired halves are 128-dim");
   using S = Slot<D>;
-  using CFG = SplitConfig<D, NT, HKV, NWH>;
+  using CFG = SplitConfig<D, NT, HKV, NWH, PH>;
   constexpr int KS = S::KS, DG = S::DG, RK = CFG::RK, RV = CFG::RV;
   __shared__ __attribute__((aligned(16))) char lds_raw[CFG::LDS_BYTES];
   lds_t *lds = (lds_t *)(lds_raw);
@@ -917,8 +1021,10 @@ void decode_split_kernel(DecodeArgs a) {
   // Wave-uniform by construction; readfirstlane tells the compiler so, which
   // keeps page lookups on the scalar unit.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int h = wave % HKV;   // KV head
+  const int h = wave % HKV;   // KV head (PH: half-head)
   const int w = wave / HKV;   // position among the NWH waves of this head
+  const int hq = PH ? h >> 1 : h;  // head of the query rows, scale planes and split state
+  const int half = PH ? h & 1 : 0;
   const int n = lane & 15, g = lane >> 4;
 
   const int role = static_cast<int>(blockIdx.x);  // this work-group's split of the plan
@@ -951,7 +1057,7 @@ void decode_split_kernel(DecodeArgs a) {
   // direct-to-LDS loads further down.
   v4i qraw[QSPLIT ? 1 : NT][KS][2];
 #pragma unroll
-  for (int nt = 0; nt < (QSPLIT ? 0 : NT); ++nt) {
+  for (int nt = 0; nt < (QSPLIT || PH ? 0 : NT); ++nt) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = (v4i){0, 0, 0, 0};
     const int r = r0 + 16 * nt + n;
@@ -969,7 +1075,7 @@ void decode_split_kernel(DecodeArgs a) {
   }
 
   WaveState<D, NT, CFG::QLDS> st;
-  lds_t *qlds = lds + CFG::Q_OFF + h * CFG::Q_BYTES_PER_HEAD;
+  lds_t *qlds = lds + CFG::Q_OFF + hq * CFG::Q_BYTES_PER_HEAD;
   // Causal ends, through scalar loads (they are uniform over the
   // work-group): row r (token j = r / 6) sees keys t < lim(r).
   int min_end = L0;
@@ -1001,7 +1107,7 @@ void decode_split_kernel(DecodeArgs a) {
   const int cnt = my0 < x1 ? (x1 - my0 + NWH - 1) / NWH : 0;
   lds_t *kring = lds + wave * CFG::WAVE_BYTES;
   lds_t *vring = kring + RK * S::K_BYTES;
-  const LaneOffsets lo = lane_offsets<D, HKV>(a, h, lane);
+  const LaneOffsets lo = lane_offsets<D, HKV, PH>(a, h, lane);
   // DMA bookkeeping (wave-uniform): `issued` counts this wave's DMA
   // instructions; mk[s] / mv[s] is the count right after the K / V group of
   // ring slot s was issued, so a chunk is resident once at most
@@ -1048,7 +1154,7 @@ void decode_split_kernel(DecodeArgs a) {
       mk[s] = issued;
     }
     if (s < RV) {
-      issue_v<D, HKV>(a, page_of(xs), xs, lo, lane, vring + s * S::V_BYTES);
+      issue_v<D, HKV, PH>(a, page_of(xs), xs, lo, lane, vring + s * S::V_BYTES);
       issued += S::NVS;
       mv[s] = issued;
     }
@@ -1059,7 +1165,7 @@ void decode_split_kernel(DecodeArgs a) {
   // a plain count of this wave's own loads.  Rows past the last query row
   // load row 0 and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if (QSPLIT && !pre_q) {
+  if (QSPLIT && !PH && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
     const char *qbase = reinterpret_cast<const char *>(a.q) + static_cast<int64_t>(b) * a.q_len * a.q_tok_stride * 2;
 #pragma unroll
@@ -1085,11 +1191,13 @@ void decode_split_kernel(DecodeArgs a) {
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
   // each wave quantizes its own tiles (nt % NWH == w) and publishes them.
-  if (pre_q) {
+  if (PH || pre_q) {
     // The tile's codes already are the B operands: lane (n, g) of tile nt
     // takes row 16 nt + n, dims 64 ks + 16 g .. + 15; dead rows stay zero.
-    const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(h) * kPage * D;
-    const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + h * kPage;
+    // (PH: the two halves of a pair stage k-steps 2 half and 2 half + 1.)
+    constexpr int DQ = CFG::DQ, KSQ = DQ / 64;
+    const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(hq) * kPage * DQ;
+    const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + hq * kPage;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if constexpr (CFG::QLDS) {
@@ -1098,23 +1206,24 @@ void decode_split_kernel(DecodeArgs a) {
       const int r = r0 + 16 * nt + n;
       const bool live = r < rows;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const v4i frag = live ? *reinterpret_cast<const v4i *>(tile + static_cast<int64_t>(r) * D + 64 * ks + 16 * g)
+      for (int ks = 0; ks < KSQ; ++ks) {
+        if (PH && (ks >> 1) != half) continue;
+        const v4i frag = live ? *reinterpret_cast<const v4i *>(tile + static_cast<int64_t>(r) * DQ + 64 * ks + 16 * g)
                               : (v4i){0, 0, 0, 0};
         if constexpr (CFG::QLDS) {
-          *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16) = frag;
+          *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KSQ + ks) * kWave + lane) * 16) = frag;
         } else {
           st.qb[nt][ks] = frag;
         }
       }
-      const double c = static_cast<double>(live ? scales[r] : 0.f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
+      const double c = static_cast<double>(live ? scales[r] : 0.f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(DQ)));
       st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
       if constexpr (CFG::QLDS) {
-        if (g == 0)
+        if (g == 0 && half == 0)
           reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
       }
     }
-  } else {
+  } else if constexpr (!PH) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -1181,6 +1290,11 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
   for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
 
+  lds_int *flags = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);  // PH: ready[WAVES] | done[WAVES]
+  if constexpr (PH) {
+    pair_flag_set(flags + wave, 0, lane);
+    pair_flag_set(flags + CFG::WAVES + wave, 0, lane);
+  }
   if constexpr (CFG::QLDS) {
     // Q fragments and row factors visible to both waves of the head.  A bare
     // barrier after the LDS writes: __syncthreads() would also wait for every
@@ -1223,17 +1337,30 @@ void decode_split_kernel(DecodeArgs a) {
       else
         wait_vm(n);
     }
+    if constexpr (PH) {
+      // This wave's half of chunk k is resident; wait for the other half.
+      pair_flag_set(flags + wave, k + 1, lane);
+      pair_flag_wait(flags + (wave ^ 1), k + 1);
+    }
     const bool valid = (valid_mask >> sk) & 1u;
     const int tbase = 32 * (my0 + k * NWH);
     v4i sc[2][NT];
-    if (valid) chunk_qk<D, NT, CFG::QLDS>(st, kslot, qlds, lane, g, sc);
+    if constexpr (PH) {
+      const lds_t *pslot = lds + (wave ^ 1) * CFG::WAVE_BYTES + sk * S::K_BYTES;
+      if (valid) chunk_qk_pair<NT>(half ? pslot : kslot, half ? kslot : pslot, qlds, lane, g, sc);
+      // Both K slots of chunk k have been read.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      pair_flag_set(flags + CFG::WAVES + wave, k + 1, lane);
+    } else {
+      if (valid) chunk_qk<D, NT, CFG::QLDS>(st, kslot, qlds, lane, g, sc);
+    }
     if (CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
       int lane_o = lane;
       asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
       const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
@@ -1243,12 +1370,14 @@ void decode_split_kernel(DecodeArgs a) {
     }
     if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end, lims);
     if (!CFG::K_EARLY && k + RK < cnt) {
-      // The K reads of this slot have completed (their values fed the MFMAs).
+      // The K reads of this slot have completed (their values fed the MFMAs);
+      // PH: so have the other half's.
+      if constexpr (PH) pair_flag_wait(flags + CFG::WAVES + (wave ^ 1), k + 1);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
       int lane_o = lane;
       asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
       const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
@@ -1261,8 +1390,8 @@ void decode_split_kernel(DecodeArgs a) {
       const int xr = my0 + (k + RV) * NWH;
       int lane_o = lane;
       asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV>(a, h, lane_o) : lo;
-      issue_v<D, HKV>(a, page_of(xr), xr, lo_r, lane, vslot);
+      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
+      issue_v<D, HKV, PH>(a, page_of(xr), xr, lo_r, lane, vslot);
       issued += S::NVS;
 #pragma unroll
       for (int s = 0; s < RV; ++s)
@@ -1326,10 +1455,12 @@ void decode_split_kernel(DecodeArgs a) {
   // dim group), then m and l in fp32.  A dequantized V value is at most
   // 15 * (65504 * 2 / 15) in magnitude, so a quarter of any average of them
   // is a finite fp16; the merge multiplies by 4 again (exact).
+  // (PH: each half writes its 128 dims of head hq's rows; m and l once.)
+  constexpr int DQ = CFG::DQ, QH = CFG::QHEADS;
   char *base = a.ws + static_cast<int64_t>(role) * a.split_bytes;
   _Float16 *obase = reinterpret_cast<_Float16 *>(base);
-  float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(HKV) * rows * D * 2);
-  float *lbase = mbase + HKV * rows;
+  float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(QH) * rows * DQ * 2);
+  float *lbase = mbase + QH * rows;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
@@ -1340,18 +1471,18 @@ void decode_split_kernel(DecodeArgs a) {
         const float f = l > 0.f ? 0.25f / l : 0.f;
 #pragma unroll
         for (int dg = 0; dg < DG; ++dg) {
-          _Float16 *dst = obase + static_cast<int64_t>(h * rows + r) * D + dg * 128 + 8 * n;
+          _Float16 *dst = obase + static_cast<int64_t>(hq * rows + r) * DQ + (half + dg) * 128 + 8 * n;
           const v8h o = {static_cast<_Float16>(st.O[nt][dg][0][i] * f), static_cast<_Float16>(st.O[nt][dg][1][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][2][i] * f), static_cast<_Float16>(st.O[nt][dg][3][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][4][i] * f), static_cast<_Float16>(st.O[nt][dg][5][i] * f),
                          static_cast<_Float16>(st.O[nt][dg][6][i] * f), static_cast<_Float16>(st.O[nt][dg][7][i] * f)};
-          *reinterpret_cast<v8h *>(dst) = o;
+          store_wt16(dst, o);
         }
-        if (n == 0) lbase[h * rows + r] = l;
+        if (n == 0 && half == 0) store_wt4(lbase + hq * rows + r, l);
       }
     }
     const int r = r0 + 16 * nt + n;
-    if (g == 0 && r < rows) mbase[h * rows + r] = st.m_run[nt];
+    if (g == 0 && half == 0 && r < rows) store_wt4(mbase + hq * rows + r, st.m_run[nt]);
   }
 }
 
@@ -1382,6 +1513,30 @@ void launch_split(DecodeArgs a, int nt, hipStream_t s) {
   }
 }
 
+// Head dim 256 with two KV heads runs as paired halves: four 128-dim
+// half-heads, two waves per SIMD (the 256-dim kernel holds one), from a query
+// quantized by its own small kernel into the workspace.
+bool paired_halves(int hkv, int head_dim) { return head_dim == 256 && hkv == 2; }
+
+void launch_split_pairs(DecodeArgs a, int nt, hipStream_t s) {
+  const dim3 grid(a.grid);
+  a.tile0 = 0;
+  switch (nt) {
+    case 1: decode_split_kernel<128, 1, 4, waves_per_head<128, 1>(), true><<<grid, dim3(256 * waves_per_head<128, 1>()), 0, s>>>(a); break;
+    case 2: decode_split_kernel<128, 2, 4, waves_per_head<128, 2>(), true><<<grid, dim3(256 * waves_per_head<128, 2>()), 0, s>>>(a); break;
+    case 3: decode_split_kernel<128, 3, 4, waves_per_head<128, 3>(), true><<<grid, dim3(256 * waves_per_head<128, 3>()), 0, s>>>(a); break;
+    default: decode_split_kernel<128, 4, 4, waves_per_head<128, 4>(), true><<<grid, dim3(256 * waves_per_head<128, 4>()), 0, s>>>(a); break;
+  }
+}
+
+// Workspace bytes ahead of the split states: the quantized query tiles and
+// their scales of a paired-halves call (256-byte aligned parts).
+int64_t query_tile_bytes(int64_t batch, int hkv, int head_dim) {
+  if (!paired_halves(hkv, head_dim)) return 0;
+  const int64_t rows = batch * hkv * kPage;
+  return ((rows * head_dim + 255) / 256) * 256 + ((rows * 4 + 255) / 256) * 256;
+}
+
 // One split's state: per KV head and query row, D fp16 outputs, then m and l.
 int64_t split_state_bytes(int hkv, int q_len, int head_dim) {
   return static_cast<int64_t>(hkv) * q_len * kGqa * (2 * head_dim + 8);
@@ -1408,8 +1563,9 @@ extern "C" int64_t k8v4_attn_workspace_bytes(int64_t batch, int64_t table_width,
   if (batch < 1 || table_width < 1 || pages_per_block < 1 || q_len < 1 || !supported_heads(hkv) ||
       !supported_dim(head_dim))
     return -1;
-  const int64_t g = choose_grid(batch, table_width, pages_per_block, hkv, INT64_MAX, num_splits);
-  return g * split_state_bytes(hkv, q_len, head_dim);
+  const int wave_heads = paired_halves(hkv, head_dim) ? 2 * hkv : hkv;
+  const int64_t g = choose_grid(batch, table_width, pages_per_block, wave_heads, INT64_MAX, num_splits);
+  return query_tile_bytes(batch, hkv, head_dim) + g * split_state_bytes(hkv, q_len, head_dim);
 }
 
 namespace k8v4 {
@@ -1465,9 +1621,11 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   K8V4_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
   if (visible_lens) K8V4_REQUIRE(vis_stride >= 1 + q_len, "visible_lens [B, 1+q_len]");
 
+  const bool pairs = paired_halves(hkv, head_dim);
+  const int64_t qt_bytes = query_tile_bytes(batch, hkv, head_dim);
   const int64_t split_bytes = split_state_bytes(hkv, q_len, head_dim);
-  const int64_t ws_splits = workspace_bytes / split_bytes;
-  const int64_t grid = choose_grid(batch, table_width, pages_per_block, hkv, ws_splits, num_splits);
+  const int64_t ws_splits = workspace_bytes > qt_bytes ? (workspace_bytes - qt_bytes) / split_bytes : 0;
+  const int64_t grid = choose_grid(batch, table_width, pages_per_block, pairs ? 2 * hkv : hkv, ws_splits, num_splits);
   if (grid > ws_splits) {
     set_error("K8/V4 workspace holds %lld split states, the batch needs at least %lld (%lld bytes each)",
               static_cast<long long>(ws_splits), static_cast<long long>(grid),
@@ -1513,7 +1671,7 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   a.batch = static_cast<int>(batch);
   a.q_len = q_len;
   a.hkv = hkv;
-  a.ws = static_cast<char *>(workspace);
+  a.ws = static_cast<char *>(workspace) + qt_bytes;
   a.split_bytes = split_bytes;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
@@ -1539,10 +1697,24 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
 
   auto s = static_cast<hipStream_t>(stream);
   if (stages & 1) {
-    if (head_dim == 128) {
+    if (pairs && !q8) {
+      // The query tiles at the head of the workspace (query_tile_bytes).
+      int8_t *tiles = static_cast<int8_t *>(workspace);
+      float *scales = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                                ((batch * hkv * kPage * head_dim + 255) / 256) * 256);
+      const int rc = q_quant_launch(q, a.q_bf16, 0, q_tok_stride, batch, q_len, hkv, head_dim, tiles, scales, s);
+      if (rc) return rc;
+      a.q8 = tiles;
+      a.q8_scale = scales;
+      a.q8_seq_stride = int64_t(hkv) * kPage * head_dim;
+      a.qs_seq_stride = int64_t(hkv) * kPage;
+    }
+    if (pairs) {
+      launch_split_pairs(a, nt, s);
+    } else if (head_dim == 128) {
       if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
     } else {
-      if (hkv == 4) launch_split<256, 4>(a, nt, s); else launch_split<256, 2>(a, nt, s);
+      launch_split<256, 4>(a, nt, s);  // (two heads run as paired halves)
     }
     const int rc = launch_status("k8v4_attn_batch split");
     if (rc) return rc;

@@ -37,6 +37,16 @@ int device_cus();
 inline bool supported_heads(int hkv) { return hkv == 2 || hkv == 4; }
 inline bool supported_dim(int d) { return d == 128 || d == 256; }
 
+// Enqueues the query quantization into Q-once tiles: per sequence b < batch
+// and KV head h, 64 rows of head_dim int8 codes at q8 + ((b * hkv + h) * 64 +
+// r) * head_dim (row r: query token r / 6 of query head h * 6 + r % 6, zero
+// past q_len tokens) and one fp32 scale per row at q_scale + (b * hkv + h) *
+// 64 + r.  Token layout: query rows [batch * q_len][6 * hkv][head_dim] with
+// q_tok_stride elements between tokens; padded layout (batch 1): the rows
+// [hkv][64][head_dim] as they are.  Arguments are not checked here.
+int q_quant_launch(const void *q, int bf16, int padded, int64_t q_tok_stride, int64_t batch, int q_len, int hkv,
+                   int head_dim, int8_t *q8, float *q_scale, hipStream_t stream);
+
 // Loads one element of a 16-bit float tensor as float (exact for fp16 and bf16).
 __device__ __forceinline__ float half_bits_to_float(uint16_t bits, bool is_bf16) {
   if (is_bf16) return __uint_as_float(static_cast<uint32_t>(bits) << 16);

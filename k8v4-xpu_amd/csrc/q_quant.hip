@@ -20,9 +20,10 @@ namespace {
 struct QQuantArgs {
   const uint16_t *q;
   int bf16;
-  int padded;          // 1: [hkv, 64, D] rows; 0: token rows [ntok, 6 * hkv, D]
+  int padded;          // 1: [hkv, 64, D] rows; 0: token rows [batch * q_len, 6 * hkv, D]
   int64_t tok_stride;  // elements between tokens (token layout)
-  int64_t ntok;
+  int64_t rows;        // tile rows: batch * hkv * 64
+  int q_len;           // query tokens per sequence (token layout)
   int hkv;
   int8_t *q8;
   float *q_scale;
@@ -34,14 +35,16 @@ __global__ __launch_bounds__(256) void q_quant_kernel(QQuantArgs a) {
   constexpr int E = D / kWave;  // elements per lane
   const int lane = threadIdx.x & (kWave - 1);
   const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x) / kWave;
-  if (row >= a.hkv * kPage) return;  // whole waves
-  const int h = row / kPage, r = row - h * kPage;
+  if (row >= a.rows) return;  // whole waves
+  const int bh = row / kPage, r = row - bh * kPage;  // bh = b * hkv + h
+  const int b = bh / a.hkv, h = bh - b * a.hkv;
   const uint16_t *src = nullptr;
   if (a.padded) {
     src = a.q + static_cast<int64_t>(row) * D;
-  } else if (r < a.ntok * kGqa) {
+  } else if (r < a.q_len * kGqa) {
     const int tok = r / kGqa;
-    src = a.q + tok * a.tok_stride + static_cast<int64_t>(h * kGqa + (r - tok * kGqa)) * D;
+    src = a.q + (static_cast<int64_t>(b) * a.q_len + tok) * a.tok_stride +
+          static_cast<int64_t>(h * kGqa + (r - tok * kGqa)) * D;
   }
   float x[E];
 #pragma unroll
@@ -65,6 +68,27 @@ __global__ __launch_bounds__(256) void q_quant_kernel(QQuantArgs a) {
 }
 
 }  // namespace
+
+int q_quant_launch(const void *q, int bf16, int padded, int64_t q_tok_stride, int64_t batch, int q_len, int hkv,
+                   int head_dim, int8_t *q8, float *q_scale, hipStream_t stream) {
+  QQuantArgs a;
+  a.q = static_cast<const uint16_t *>(q);
+  a.bf16 = bf16;
+  a.padded = padded;
+  a.tok_stride = q_tok_stride;
+  a.rows = batch * hkv * kPage;
+  a.q_len = q_len;
+  a.hkv = hkv;
+  a.q8 = q8;
+  a.q_scale = q_scale;
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  if (head_dim == 128)
+    q_quant_kernel<128><<<grid, dim3(256), 0, stream>>>(a);
+  else
+    q_quant_kernel<256><<<grid, dim3(256), 0, stream>>>(a);
+  return launch_status("k8v4 query quantization");
+}
+
 }  // namespace k8v4
 
 extern "C" int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_tok_stride, int64_t ntok, int hkv,
@@ -84,20 +108,7 @@ extern "C" int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_to
                "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
   K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q8) % 4 == 0 && reinterpret_cast<uintptr_t>(q_scale) % 4 == 0,
                "q8 / q_scale misaligned");
-  QQuantArgs a;
-  a.q = static_cast<const uint16_t *>(q);
-  a.bf16 = q_dtype == K8V4_BF16;
-  a.padded = layout == K8V4_Q_PADDED;
-  a.tok_stride = q_tok_stride;
-  a.ntok = ntok;
-  a.hkv = hkv;
-  a.q8 = q8;
-  a.q_scale = q_scale;
-  const dim3 grid(static_cast<unsigned>(hkv * kPage / 4));
-  auto s = static_cast<hipStream_t>(stream);
-  if (head_dim == 128)
-    q_quant_kernel<128><<<grid, dim3(256), 0, s>>>(a);
-  else
-    q_quant_kernel<256><<<grid, dim3(256), 0, s>>>(a);
-  return launch_status("k8v4_q_quant");
+  return q_quant_launch(q, q_dtype == K8V4_BF16, layout == K8V4_Q_PADDED, q_tok_stride, 1,
+                        layout == K8V4_Q_TOKENS ? static_cast<int>(ntok) : 0, hkv, head_dim, q8, q_scale,
+                        static_cast<hipStream_t>(stream));
 }

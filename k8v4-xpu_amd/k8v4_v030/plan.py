@@ -110,9 +110,19 @@ def split_state_bytes(q_len: int, layout: PageLayout) -> int:
     return layout.hkv * rows * (2 * layout.head_dim + 8)
 
 
-def attn_workspace_bytes(max_splits: int, q_len: int, layout: PageLayout) -> int:
-    """Scratch the decode kernel needs for ``max_splits`` split-K work-groups."""
-    return int(max_splits) * split_state_bytes(q_len, layout)
+def query_tile_bytes(batch: int, layout: PageLayout) -> int:
+    """Workspace head of a 256-dim, two-KV-head decode (its query runs through a
+    quantization kernel first): per sequence and KV head 64 rows of int8 codes,
+    then their fp32 scales, each part rounded up to 256 bytes; 0 otherwise."""
+    if not (layout.head_dim == 256 and layout.hkv == 2):
+        return 0
+    rows = int(batch) * layout.hkv * PAGE
+    return -(-rows * layout.head_dim // 256) * 256 + -(-rows * 4 // 256) * 256
+
+
+def attn_workspace_bytes(max_splits: int, q_len: int, layout: PageLayout, batch: int = 1) -> int:
+    """Scratch the decode kernel needs for ``max_splits`` split-K work-groups over ``batch`` sequences."""
+    return query_tile_bytes(batch, layout) + int(max_splits) * split_state_bytes(q_len, layout)
 
 
 def layout_for_heads(num_heads: int, num_kv_heads: int, head_size: int) -> PageLayout:
@@ -153,6 +163,7 @@ def require_decoder(
 __all__ = [
     "PAGE",
     "attn_workspace_bytes",
+    "query_tile_bytes",
     "layout_for_heads",
     "query_lengths",
     "query_segments",

@@ -100,14 +100,18 @@ def test_workspace_bytes_match_the_python_sizing(lib, hkv, d, q_len, splits):
     """The host-side sizing (plan.attn_workspace_bytes, used by the backend's
     scratch) and the library agree for an explicit split count."""
     from k8v4_v030.layout import PageLayout
-    from k8v4_v030.plan import attn_workspace_bytes, split_state_bytes
+    from k8v4_v030.plan import attn_workspace_bytes, query_tile_bytes, split_state_bytes
 
     lay = PageLayout(hkv, d)
     got = lib.k8v4_attn_workspace_bytes(1, 4096, 1, q_len, hkv, d, splits)
-    assert got == attn_workspace_bytes(splits, q_len, lay) == splits * split_state_bytes(q_len, lay)
+    head = query_tile_bytes(1, lay)
+    assert got == attn_workspace_bytes(splits, q_len, lay) == head + splits * split_state_bytes(q_len, lay)
+    # Only the paired-halves shape (head dim 256, two KV heads) quantizes its
+    # query into the workspace: 64 rows of 256 codes and 64 scales per head.
+    assert head == (2 * 64 * 256 + 512 if (hkv, d) == (2, 256) else 0)
     assert split_state_bytes(q_len, lay) % 16 == 0  # every split state starts 16-byte aligned
     # The grid never has fewer splits than sequences.
-    assert lib.k8v4_attn_workspace_bytes(8, 4096, 1, q_len, hkv, d, 3) == attn_workspace_bytes(8, q_len, lay)
+    assert lib.k8v4_attn_workspace_bytes(8, 4096, 1, q_len, hkv, d, 3) == attn_workspace_bytes(8, q_len, lay, 8)
 
 
 def test_ops_layer_raises_without_gpu_tensors(lib):

@@ -336,26 +336,28 @@ def test_zero_length_rows_and_output_dtypes(gpu_ops):
     assert assert_close(outbf32.cpu().numpy(), want_bf, what="bf16 q, fp32 out") < 5e-4
 
 
-def test_values_near_the_fp16_limit_survive_the_split_states(gpu_ops):
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+def test_values_near_the_fp16_limit_survive_the_split_states(gpu_ops, hkv, d):
     """Every 7th token's V row alternates 60000 / -65504, whose -65504 codes
     dequantize beyond the fp16 range (-8 * 125504 / 15 = -66935), and its K row draws
     almost all of the softmax weight: the outputs exceed 65504 in magnitude.
     The split states (fp16, a quarter of each split's normalized output) and
     their merge must stay finite and match the oracle for fp32 output."""
-    lay = PageLayout(4, 128)
+    print("large V hkv=%d d=%d" % (hkv, d), flush=True)
+    lay = PageLayout(hkv, d)
     cache = Cache(64, lay)
     gen = torch.Generator().manual_seed(41)
     table = random_tables(gen, [3000], 64)
     L = 3000
     t = torch.arange(L)
     slots = (table[0].long()[t // PAGE] * PAGE + t % PAGE).to(DEV)
-    k = seeded_normal(gen, (L, 4, 128))
-    v = seeded_normal(gen, (L, 4, 128))
+    k = seeded_normal(gen, (L, hkv, d))
+    v = seeded_normal(gen, (L, hkv, d))
     k[::7] = 4.0
     v[::7, :, 0::2] = 60000.0
     v[::7, :, 1::2] = -65504.0
     cache.store(gpu_ops, k.to(DEV), v.to(DEV), slots)
-    q = seeded_normal(gen, (3, 24, 128)).abs()
+    q = seeded_normal(gen, (3, 6 * hkv, d)).abs()
     seq = torch.tensor([L])
     want = _oracle(cache, q, table, seq, 3)
     assert np.abs(want).max() > 65504.0
