@@ -255,15 +255,17 @@ __device__ __forceinline__ int physical_page(const DecodeArgs &a, const int32_t 
 // ------------------------------------------------------------ merge
 // The splits of one sequence are combined per output row (token, query
 // head): a merge unit is one column slice of one row, VPR = D / 8 / merge_cs
-// columns of 8 dims, folded over the sequence's split states by the TPU = 128
-// threads of one work-group.  Thread t owns column t % VPR and the splits
-// t / VPR + k * SPI
-// (SPI = TPU / VPR); it loads the (m, l, O) of up to MU of its splits at
-// once and folds them online (running max, rescaled sums), one round trip per
-// MU splits; the per-thread partial states are then combined in LDS with the
-// same rescaling.
+// columns of 8 dims (at least 8 columns: 128-byte state lines are never
+// shared between units), folded over the sequence's split states by the TPU
+// threads (128 or 256) of one work-group.  Thread t owns column t % VPR and
+// the splits t / VPR + k * SPI (SPI = TPU / VPR); it loads the (m, l, O) of
+// up to MU of its splits at once and folds them online (running max,
+// rescaled sums), one round trip per MU splits (the host picks TPU and
+// merge_cs so that one round covers the average sequence).  The threads of a
+// column are then combined with the same rescaling: within a wave by lane
+// exchanges, across the waves through a few LDS words.
 
-constexpr int kMergeTPU = 128;
+constexpr int kMergeMU = 8;  // splits loaded together by one merge thread
 
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, float v) {
   if (dtype == K8V4_F32)
@@ -275,6 +277,7 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
 }
 
 typedef float v8f __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // Where one merge unit's row lives.
 struct MergeRow {
@@ -293,114 +296,129 @@ __device__ __forceinline__ MergeRow merge_row(const DecodeArgs &a, int unit) {
   return m;
 }
 
-// LDS of one merge unit: TPU partial outputs, then SPI running maxima and sums.
-template <int TPU>
-constexpr int merge_lds_bytes() { return TPU * 32 + 2 * TPU * 4; }
+// Running (max, sum, output) of one column, folded online.
+struct MergeAcc {
+  float M, l;
+  v8f o;
+};
 
-// Phase 1: fold this thread's splits and leave its partial state in LDS.
-template <int D, int TPU>
-__device__ void merge_fold(const DecodeArgs &a, int unit, int t, int first, int count, char *red) {
-  constexpr int MU = 8;  // splits loaded together by one thread
-  const int VPR = (D / 8) / a.merge_cs;
-  const int SPI = TPU / VPR;
-  const int col = t % VPR, sg = t / VPR;
-  v8f *red_o = reinterpret_cast<v8f *>(red);
-  float *red_m = reinterpret_cast<float *>(red + TPU * 32);
-  float *red_l = red_m + TPU;
-  float M = -INFINITY, lacc = 0.f;
-  v8f acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (unit >= 0) {
-    const MergeRow mr = merge_row(a, unit);
-    const int rows = a.q_len * kGqa;
-    const int dcol = 8 * (mr.slice * VPR + col);
-    // Byte offsets inside one split state (layout written by the split kernel).
-    const int64_t o_off = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
-    const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
-    const int64_t l_off = m_off + a.hkv * rows * 4;
-    const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
-    for (int s0 = sg; s0 < count; s0 += MU * SPI) {
-      float ms[MU], ls[MU];
-      v8f os[MU];
+// Folds this thread's splits (sg, sg + SPI, ...) of the unit's column.
+template <int D>
+__device__ __forceinline__ MergeAcc merge_fold(const DecodeArgs &a, const MergeRow &mr, int col, int sg, int SPI,
+                                               int VPR, int first, int count) {
+  MergeAcc acc{-INFINITY, 0.f, (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
+  const int rows = a.q_len * kGqa;
+  const int dcol = 8 * (mr.slice * VPR + col);
+  // Byte offsets inside one split state (layout written by the split kernel).
+  const int64_t o_off = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
+  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
+  const int64_t l_off = m_off + a.hkv * rows * 4;
+  const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
+  for (int s0 = sg; s0 < count; s0 += kMergeMU * SPI) {
+    float ms[kMergeMU], ls[kMergeMU];
+    v8f os[kMergeMU];
 #pragma unroll
-      for (int u = 0; u < MU; ++u) {
-        const int s = s0 + u * SPI;
-        ms[u] = -INFINITY;
-        ls[u] = 0.f;
-        os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (s < count) {
-          const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-          // Default-policy loads: the states were written by the split kernel
-          // just before, and nontemporal loads of them measured slower.
-          ms[u] = *reinterpret_cast<const float *>(st + m_off);
-          ls[u] = *reinterpret_cast<const float *>(st + l_off);
-          os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + o_off), v8f);
-        }
-      }
-      float mn = M;
-#pragma unroll
-      for (int u = 0; u < MU; ++u) mn = fmaxf(mn, ms[u]);
-      if (mn != -INFINITY) {
-        const float c = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
-        lacc *= c;
-        acc *= c;
-#pragma unroll
-        for (int u = 0; u < MU; ++u) {
-          const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
-          lacc += w;
-          acc += (4.f * w) * os[u];
-        }
-        M = mn;
+    for (int u = 0; u < kMergeMU; ++u) {
+      const int s = s0 + u * SPI;
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
+      os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (s < count) {
+        const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
+        ms[u] = *reinterpret_cast<const float *>(st + m_off);
+        ls[u] = *reinterpret_cast<const float *>(st + l_off);
+        os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + o_off), v8f);
       }
     }
+    float mn = acc.M;
+#pragma unroll
+    for (int u = 0; u < kMergeMU; ++u) mn = fmaxf(mn, ms[u]);
+    if (mn != -INFINITY) {
+      const float c = acc.M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc.M - mn);
+      acc.l *= c;
+      acc.o *= c;
+#pragma unroll
+      for (int u = 0; u < kMergeMU; ++u) {
+        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
+        acc.l += w;
+        acc.o += (4.f * w) * os[u];  // the states hold a quarter of the split's output
+      }
+      acc.M = mn;
+    }
   }
-  red_o[t] = acc;
-  if (col == 0) {
-    red_m[sg] = M;
-    red_l[sg] = lacc;
-  }
+  return acc;
 }
 
-// Phase 2 (after a barrier): combine the SPI partial states of each column
-// and store the row's outputs.
-template <int D, int TPU>
-__device__ void merge_finish(const DecodeArgs &a, int unit, int t, const char *red) {
-  const int VPR = (D / 8) / a.merge_cs;
-  const int SPI = TPU / VPR;
-  if (unit < 0 || t >= VPR) return;
-  const v8f *red_o = reinterpret_cast<const v8f *>(red);
-  const float *red_m = reinterpret_cast<const float *>(red + TPU * 32);
-  const float *red_l = red_m + TPU;
-  float Mg = -INFINITY;
-  for (int g2 = 0; g2 < SPI; ++g2) Mg = fmaxf(Mg, red_m[g2]);
-  float l = 0.f;
-  v8f o = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (Mg != -INFINITY) {
-    for (int g2 = 0; g2 < SPI; ++g2) {
-      const float mg = red_m[g2];
-      const float w = mg == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg - Mg);
-      l += w * red_l[g2];
-      o += w * red_o[g2 * VPR + t];
-    }
-  }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  const MergeRow mr = merge_row(a, unit);
-  const int64_t ob = static_cast<int64_t>(mr.tok) * a.out_tok_stride + static_cast<int64_t>(mr.qh) * D +
-                     8 * (mr.slice * VPR + t);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) store_out(a.out, a.out_dtype, ob + e, o[e] * inv);
+// Rescales an accumulator to the reference max Mr (Mr >= M; both -inf: empty).
+__device__ __forceinline__ void merge_rescale(MergeAcc &x, float Mr) {
+  const float w = x.M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x.M - Mr);
+  x.l *= w;
+  x.o *= w;
+  x.M = Mr;
 }
 
 // The merge kernel: one unit per work-group.
-template <int D>
-__global__ __launch_bounds__(kMergeTPU) void decode_merge_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char red[merge_lds_bytes<kMergeTPU>()];
+template <int D, int TPU>
+__global__ __launch_bounds__(TPU) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int NW = TPU / kWave;
+  __shared__ float red[NW > 1 ? NW * 32 * 10 : 1];  // per wave and column: M, l, o[8]
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   const int unit = static_cast<int>(blockIdx.x);
   const int P = plan_pages_per_split(a, lane);
-  const SplitRange sr = plan_locate(a, P, lane, merge_row(a, unit).b, -1);
-  merge_fold<D, kMergeTPU>(a, unit, threadIdx.x, sr.first, sr.b < 0 ? 0 : sr.count, red);
-  __syncthreads();
-  merge_finish<D, kMergeTPU>(a, unit, threadIdx.x, red);
+  const MergeRow mr = merge_row(a, unit);
+  const SplitRange sr = plan_locate(a, P, lane, mr.b, -1);
+  const int VPR = (D / 8) / a.merge_cs;
+  const int SPI = TPU / VPR;
+  const int t = threadIdx.x, col = t % VPR, sg = t / VPR;
+  MergeAcc acc = merge_fold<D>(a, mr, col, sg, SPI, VPR, sr.first, sr.b < 0 ? 0 : sr.count);
+  // The lanes of one column in a wave are col + VPR * j: combine them.
+  float Mw = acc.M;
+  for (int off = VPR; off < kWave; off <<= 1) Mw = fmaxf(Mw, __shfl_xor(Mw, off, kWave));
+  merge_rescale(acc, Mw);
+  for (int off = VPR; off < kWave; off <<= 1) {
+    acc.l += __shfl_xor(acc.l, off, kWave);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc.o[e] += __shfl_xor(acc.o[e], off, kWave);
+  }
+  if constexpr (NW > 1) {
+    // Then the waves: each publishes its columns, wave 0 folds them.
+    if (lane < VPR) {
+      float *w = red + (wave * 32 + lane) * 10;
+      w[0] = acc.M;
+      w[1] = acc.l;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[2 + e] = acc.o[e];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float Mg = acc.M;
+#pragma unroll
+    for (int v = 1; v < NW; ++v) Mg = fmaxf(Mg, red[(v * 32 + (lane & 31)) * 10]);
+    merge_rescale(acc, Mg);
+#pragma unroll
+    for (int v = 1; v < NW; ++v) {
+      const float *w = red + (v * 32 + (lane & 31)) * 10;
+      MergeAcc x{w[0], w[1], (v8f){w[2], w[3], w[4], w[5], w[6], w[7], w[8], w[9]}};
+      merge_rescale(x, Mg);
+      acc.l += x.l;
+      acc.o += x.o;
+    }
+  }
+  if (unit < 0 || lane >= VPR) return;
+  const float inv = acc.l > 0.f ? 1.f / acc.l : 0.f;
+  const int64_t ob = static_cast<int64_t>(mr.tok) * a.out_tok_stride + static_cast<int64_t>(mr.qh) * D +
+                     8 * (mr.slice * VPR + lane);
+  const v8f o = acc.o * inv;
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.out) + static_cast<uintptr_t>(ob) * (a.out_dtype == K8V4_F32 ? 4 : 2);
+  if (a.out_dtype == K8V4_F16 && addr % 16 == 0) {
+    *reinterpret_cast<v8h *>(addr) = __builtin_convertvector(o, v8h);
+  } else if (a.out_dtype == K8V4_BF16 && addr % 16 == 0) {
+    *reinterpret_cast<v8bf *>(addr) = __builtin_convertvector(o, v8bf);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) store_out(a.out, a.out_dtype, ob + e, o[e]);
+  }
 }
 
 // ------------------------------------------------------------ split kernel
@@ -1675,18 +1693,30 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   a.split_bytes = split_bytes;
   a.grid = static_cast<int>(grid);
   a.min_pages = 1;
-  // Merge units of 128 threads, one per merge work-group.  Column slices per
-  // output row: enough that a merge thread folds at most 16 splits of a
-  // sequence with the average split count G / batch (one long sequence can
-  // own all G splits); one slice per row otherwise, since every extra unit
-  // repeats the plan.
+  // Merge units: one work-group of TPU threads per column slice of an
+  // output row.  The fewest slices (at least 8 columns of 8 dims each) and
+  // the smaller work-group with which one thread folds at most one round of
+  // kMergeMU splits of a sequence with the average split count G / batch
+  // (one long sequence can own all G splits); otherwise the most threads per
+  // column.
   const int nt = (q_len * kGqa + 15) / 16;
-  const int tpu = kMergeTPU;
+  int merge_tpu = 256;
   {
-    const int vpr = head_dim / 8;
+    const int vpr_max = head_dim / 8;
     const int64_t avg = (a.grid + batch - 1) / batch;
-    int cs = 1;
-    while (vpr / cs > 4 && (tpu / (vpr / cs)) * 16 < avg) cs *= 2;
+    int cs = vpr_max / 8;
+    bool found = false;
+    for (int tpu : {128, 256}) {
+      for (int c = 1; vpr_max / c >= 8 && !found; c *= 2) {
+        const int spi = tpu / (vpr_max / c);
+        if ((avg + spi - 1) / spi <= kMergeMU) {
+          cs = c;
+          merge_tpu = tpu;
+          found = true;
+        }
+      }
+      if (found) break;
+    }
     a.merge_cs = cs;
   }
   K8V4_REQUIRE(batch * q_len * kGqa * hkv * a.merge_cs <= INT32_MAX / 2, "batch too large for one merge launch");
@@ -1728,10 +1758,17 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
   }
   if (!(stages & 2)) return K8V4_OK;
   const dim3 mgrid(static_cast<unsigned>(a.units));
-  if (head_dim == 128)
-    decode_merge_kernel<128><<<mgrid, dim3(kMergeTPU), 0, s>>>(a);
-  else
-    decode_merge_kernel<256><<<mgrid, dim3(kMergeTPU), 0, s>>>(a);
+  if (merge_tpu == 128) {
+    if (head_dim == 128)
+      decode_merge_kernel<128, 128><<<mgrid, dim3(128), 0, s>>>(a);
+    else
+      decode_merge_kernel<256, 128><<<mgrid, dim3(128), 0, s>>>(a);
+  } else {
+    if (head_dim == 128)
+      decode_merge_kernel<128, 256><<<mgrid, dim3(256), 0, s>>>(a);
+    else
+      decode_merge_kernel<256, 256><<<mgrid, dim3(256), 0, s>>>(a);
+  }
   return launch_status("k8v4_attn_batch merge");
 }
 
