@@ -1202,14 +1202,53 @@ void decode_split_kernel(DecodeArgs a) {
       }
     }
   }
+  // PH: the query tile's fragments go by direct-to-LDS loads straight into
+  // their operand positions (lane L of fragment (nt, ks) is 16 bytes at 16 L:
+  // row 16 nt + n, dims 64 ks + 16 g), the rows' scales into the factor
+  // words; no K slot stages anything, so the whole ring is filled at once.
+  if constexpr (PH) {
+    constexpr int DQ = CFG::DQ, KSQ = DQ / 64;
+    const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(hq) * kPage * DQ;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt % NWH != w) continue;
+#pragma unroll
+      for (int ks = 2 * half; ks < 2 * half + 2; ++ks) {
+        dma16s(tile, static_cast<uint32_t>((r0 + 16 * nt + n) * DQ + 64 * ks + 16 * g),
+               qlds + (nt * KSQ + ks) * kWave * 16);
+        ++issued;
+      }
+    }
+    if (w == 0 && half == 0) {
+      const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + hq * kPage;
+      if (lane < NT * 16) dma4s(scales, static_cast<uint32_t>((r0 + lane) * 4), qlds + CFG::Q_FRAG_BYTES);
+      ++issued;
+    }
+  }
   const int q_done = issued;
   fill_slot(0);
-  if constexpr (QSPLIT) wait_vm(issued - q_done);
+  if constexpr (PH) {
+#pragma unroll
+    for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
+  }
+  if constexpr (QSPLIT || PH) wait_vm(issued - q_done);
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
   // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
   // each wave quantizes its own tiles (nt % NWH == w) and publishes them.
-  if (PH || pre_q) {
+  if constexpr (PH) {
+    // Rows past the live ones: zero operands (a caller's tile may hold
+    // anything in its padding rows).
+    constexpr int KSQ = CFG::DQ / 64;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt % NWH != w || r0 + 16 * nt + n < rows) continue;
+#pragma unroll
+      for (int ks = 2 * half; ks < 2 * half + 2; ++ks)
+        *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KSQ + ks) * kWave + lane) * 16) =
+            (v4i){0, 0, 0, 0};
+    }
+  } else if (pre_q) {
     // The tile's codes already are the B operands: lane (n, g) of tile nt
     // takes row 16 nt + n, dims 64 ks + 16 g .. + 15; dead rows stay zero.
     // (PH: the two halves of a pair stage k-steps 2 half and 2 half + 1.)
@@ -1305,8 +1344,10 @@ void decode_split_kernel(DecodeArgs a) {
 
   // The staged query rows have been read (their values are quantized).
   if constexpr (CFG::QLDS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if constexpr (!PH) {
 #pragma unroll
-  for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
+    for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
+  }
 
   lds_int *flags = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);  // PH: ready[WAVES] | done[WAVES]
   if constexpr (PH) {
@@ -1320,8 +1361,16 @@ void decode_split_kernel(DecodeArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      st.crow[nt] = reinterpret_cast<const __attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n];
+    for (int nt = 0; nt < NT; ++nt) {
+      const float f = reinterpret_cast<const __attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n];
+      if constexpr (PH) {
+        // f is the row's quantization scale (dead rows: zero operands, any factor)
+        const double c = static_cast<double>(f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(CFG::DQ)));
+        st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+      } else {
+        st.crow[nt] = f;
+      }
+    }
   }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
