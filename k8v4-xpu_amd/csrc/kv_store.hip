@@ -20,6 +20,9 @@
 // group, so fewer, wider lanes per pair cut the instruction count per byte.
 #include "k8v4_common.h"
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 namespace k8v4 {
 namespace {
 
@@ -161,10 +164,14 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
       kw[i >> 2] |= b << (8 * (i & 3));
     }
   }
+  // Code rows are written with the nontemporal policy: nothing reads them
+  // back in this kernel, and streaming them past the L2 leaves no dirty lines
+  // for the end-of-kernel write-back (4 x 4,224 tokens: 17.5 -> 15.3 us).
   char *kdst = reinterpret_cast<char *>(a.k_cache) + page * a.k_ps + cell * D + E * sub;
 #pragma unroll
   for (int c = 0; c < E / 16; ++c)
-    reinterpret_cast<uint4 *>(kdst)[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
+    __builtin_nontemporal_store((u32x4){kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]},
+                                reinterpret_cast<u32x4 *>(kdst) + c);
   if (sub == 0)
     *reinterpret_cast<float *>(reinterpret_cast<char *>(a.k_scale) + page * a.ks_ps + cell * 4) =
         static_cast<float>(k_scale);
@@ -191,7 +198,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   }
 
   char *vdst = reinterpret_cast<char *>(a.v_cache) + page * a.v_ps + cell * (D / 2) + (E / 2) * sub;
-  *reinterpret_cast<uint2 *>(vdst) = make_uint2(vw[0], vw[1]);
+  __builtin_nontemporal_store((u32x2){vw[0], vw[1]}, reinterpret_cast<u32x2 *>(vdst));
   if (sub == 0) {
     *reinterpret_cast<float *>(reinterpret_cast<char *>(a.v_scale) + page * a.vs_ps + cell * 4) =
         static_cast<float>(v_scale);
