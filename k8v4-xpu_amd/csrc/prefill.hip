@@ -677,7 +677,20 @@ __device__ __forceinline__ PPVIn pp_fetch_v(const char *stage, const PPLane &L) 
   return in;
 }
 
+// Stores of a tile image: to LDS, or (NT) to the workspace with the
+// nontemporal policy, which leaves no dirty lines in L2 for the end of the
+// conversion kernel to write back (the next kernel reads the tiles through
+// other XCDs' caches anyway).
+template <bool NT, typename T>
+__device__ __forceinline__ void tile_store(char *dst, T v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(v, reinterpret_cast<T *>(dst));
+  else
+    *reinterpret_cast<T *>(dst) = v;
+}
+
 // K chunk of tile page p: fp16 codes times k_scale * c (zero past the sequence).
+template <bool NT = false>
 __device__ __forceinline__ void pp_emit_k(const PrefillArgs &a, int p, const PPKIn &in, char *buf, int kc_dst, int key) {
   const float kc = p * 64 + key < a.seq_len ? in.ks * a.c : 0.f;
   const v2h kc2 = {static_cast<_Float16>(kc), static_cast<_Float16>(kc)};
@@ -688,11 +701,12 @@ __device__ __forceinline__ void pp_emit_k(const PrefillArgs &a, int p, const PPK
   k_codes_to_f16(in.k.w, h[6], h[7]);
 #pragma unroll
   for (int e = 0; e < 8; ++e) h[e] *= kc2;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   char *row = buf + kc_dst;
-  *reinterpret_cast<uint4 *>(row) = make_uint4(__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
-                                               __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3]));
-  *reinterpret_cast<uint4 *>(row + 16) = make_uint4(__builtin_bit_cast(uint32_t, h[4]), __builtin_bit_cast(uint32_t, h[5]),
-                                                    __builtin_bit_cast(uint32_t, h[6]), __builtin_bit_cast(uint32_t, h[7]));
+  tile_store<NT>(row, (u32x4){__builtin_bit_cast(uint32_t, h[0]), __builtin_bit_cast(uint32_t, h[1]),
+                              __builtin_bit_cast(uint32_t, h[2]), __builtin_bit_cast(uint32_t, h[3])});
+  tile_store<NT>(row + 16, (u32x4){__builtin_bit_cast(uint32_t, h[4]), __builtin_bit_cast(uint32_t, h[5]),
+                                   __builtin_bit_cast(uint32_t, h[6]), __builtin_bit_cast(uint32_t, h[7])});
 }
 
 // V item of tile page p, dequantized: each V^T entry is (nibble - v_zero) *
@@ -701,6 +715,7 @@ __device__ __forceinline__ void pp_emit_k(const PrefillArgs &a, int p, const PPK
 // factors).  The 1/16 keeps every V row of fp16 range (and 16 times more) a
 // finite fp16; the output multiplies it back.  Keys past the sequence become
 // zeros.
+template <bool NT = false>
 __device__ __forceinline__ void pp_emit_v(const PrefillArgs &a, int p, const PPVIn &in, char *buf, const PPLane &L) {
   const bool live0 = p * 64 + L.vkey < a.seq_len, live1 = p * 64 + L.vkey + 1 < a.seq_len;
   const float s0 = live0 ? in.vs.x * 0.0625f : 0.f, s1 = live1 ? in.vs.y * 0.0625f : 0.f;
@@ -719,8 +734,8 @@ __device__ __forceinline__ void pp_emit_v(const PrefillArgs &a, int p, const PPV
     ye[1] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xe[1]), se1, ce1));
     yo[0] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xo[0]), so0, co0));
     yo[1] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(xo[1]), so1, co1));
-    *reinterpret_cast<v2h *>(vrow + (2 * b) * PP::VROW) = ye;
-    *reinterpret_cast<v2h *>(vrow + (2 * b + 1) * PP::VROW) = yo;
+    tile_store<NT>(vrow + (2 * b) * PP::VROW, ye);
+    tile_store<NT>(vrow + (2 * b + 1) * PP::VROW, yo);
   }
 }
 
@@ -1167,12 +1182,12 @@ __global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, cha
     PPKIn in;
     in.k = *reinterpret_cast<const uint4 *>(kb + key * krow + 16 * part);
     in.ks = reinterpret_cast<const float *>(st + PP::SS_OFF)[key];
-    pp_emit_k(a, p, in, buf, key * PP::KROW + 32 * part, key);
+    pp_emit_k<true>(a, p, in, buf, key * PP::KROW + 32 * part, key);
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const PPLane L = pp_lane(a, t, 0, r, 0);
-    pp_emit_v(a, p, pp_fetch_v(st, L), buf, L);
+    pp_emit_v<true>(a, p, pp_fetch_v(st, L), buf, L);
   }
 }
 
