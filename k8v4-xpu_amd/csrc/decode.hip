@@ -302,49 +302,75 @@ struct MergeAcc {
   v8f o;
 };
 
+// One round of a merge thread: the (m, l, O) of its splits s = s0 + u * SPI
+// (u < kMergeMU) below `limit`, others empty.
+struct MergeRound {
+  float ms[kMergeMU], ls[kMergeMU];
+  v8f os[kMergeMU];
+};
+
+// Byte offsets of a unit's column inside one split state (layout written by
+// the split kernel: O [hkv][rows][D] fp16, then m and l [hkv][rows] fp32).
+struct MergeOffsets {
+  int64_t o, m, l;
+};
+template <int D>
+__device__ __forceinline__ MergeOffsets merge_offsets(const DecodeArgs &a, const MergeRow &mr, int col, int VPR) {
+  const int rows = a.q_len * kGqa;
+  const int dcol = 8 * (mr.slice * VPR + col);
+  MergeOffsets o;
+  o.o = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
+  o.m = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
+  o.l = o.m + a.hkv * rows * 4;
+  return o;
+}
+
+__device__ __forceinline__ void merge_load(const DecodeArgs &a, const MergeOffsets &off, const char *ws, int s0,
+                                           int SPI, int limit, MergeRound &rd) {
+#pragma unroll
+  for (int u = 0; u < kMergeMU; ++u) {
+    const int s = s0 + u * SPI;
+    rd.ms[u] = -INFINITY;
+    rd.ls[u] = 0.f;
+    rd.os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (s < limit) {
+      const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
+      rd.ms[u] = *reinterpret_cast<const float *>(st + off.m);
+      rd.ls[u] = *reinterpret_cast<const float *>(st + off.l);
+      rd.os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + off.o), v8f);
+    }
+  }
+}
+
+__device__ __forceinline__ void merge_fold_round(MergeAcc &acc, const MergeRound &rd) {
+  float mn = acc.M;
+#pragma unroll
+  for (int u = 0; u < kMergeMU; ++u) mn = fmaxf(mn, rd.ms[u]);
+  if (mn != -INFINITY) {
+    const float c = acc.M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc.M - mn);
+    acc.l *= c;
+    acc.o *= c;
+#pragma unroll
+    for (int u = 0; u < kMergeMU; ++u) {
+      const float w = rd.ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(rd.ms[u] - mn) * rd.ls[u];
+      acc.l += w;
+      acc.o += (4.f * w) * rd.os[u];  // the states hold a quarter of the split's output
+    }
+    acc.M = mn;
+  }
+}
+
 // Folds this thread's splits (sg, sg + SPI, ...) of the unit's column.
 template <int D>
 __device__ __forceinline__ MergeAcc merge_fold(const DecodeArgs &a, const MergeRow &mr, int col, int sg, int SPI,
                                                int VPR, int first, int count) {
   MergeAcc acc{-INFINITY, 0.f, (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
-  const int rows = a.q_len * kGqa;
-  const int dcol = 8 * (mr.slice * VPR + col);
-  // Byte offsets inside one split state (layout written by the split kernel).
-  const int64_t o_off = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
-  const int64_t m_off = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
-  const int64_t l_off = m_off + a.hkv * rows * 4;
+  const MergeOffsets off = merge_offsets<D>(a, mr, col, VPR);
   const char *ws = a.ws + static_cast<int64_t>(first) * a.split_bytes;
   for (int s0 = sg; s0 < count; s0 += kMergeMU * SPI) {
-    float ms[kMergeMU], ls[kMergeMU];
-    v8f os[kMergeMU];
-#pragma unroll
-    for (int u = 0; u < kMergeMU; ++u) {
-      const int s = s0 + u * SPI;
-      ms[u] = -INFINITY;
-      ls[u] = 0.f;
-      os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (s < count) {
-        const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-        ms[u] = *reinterpret_cast<const float *>(st + m_off);
-        ls[u] = *reinterpret_cast<const float *>(st + l_off);
-        os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + o_off), v8f);
-      }
-    }
-    float mn = acc.M;
-#pragma unroll
-    for (int u = 0; u < kMergeMU; ++u) mn = fmaxf(mn, ms[u]);
-    if (mn != -INFINITY) {
-      const float c = acc.M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc.M - mn);
-      acc.l *= c;
-      acc.o *= c;
-#pragma unroll
-      for (int u = 0; u < kMergeMU; ++u) {
-        const float w = ms[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mn) * ls[u];
-        acc.l += w;
-        acc.o += (4.f * w) * os[u];  // the states hold a quarter of the split's output
-      }
-      acc.M = mn;
-    }
+    MergeRound rd;
+    merge_load(a, off, ws, s0, SPI, count, rd);
+    merge_fold_round(acc, rd);
   }
   return acc;
 }
@@ -365,13 +391,35 @@ __global__ __launch_bounds__(TPU) void decode_merge_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int unit = static_cast<int>(blockIdx.x);
-  const int P = plan_pages_per_split(a, lane);
   const MergeRow mr = merge_row(a, unit);
-  const SplitRange sr = plan_locate(a, P, lane, mr.b, -1);
   const int VPR = (D / 8) / a.merge_cs;
   const int SPI = TPU / VPR;
   const int t = threadIdx.x, col = t % VPR, sg = t / VPR;
-  MergeAcc acc = merge_fold<D>(a, mr, col, sg, SPI, VPR, sr.first, sr.b < 0 ? 0 : sr.count);
+  MergeAcc acc{-INFINITY, 0.f, (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
+  if (a.batch == 1 && a.grid <= kMergeMU * SPI) {
+    // One sequence owns splits 0 .. count - 1 of the G, and one round covers
+    // all G: the states of every split that can exist are loaded before the
+    // plan, so their round trip overlaps the one for the lengths; splits
+    // past the plan's count (stale states) are dropped afterwards.
+    MergeRound rd;
+    merge_load(a, merge_offsets<D>(a, mr, col, VPR), a.ws, sg, SPI, a.grid, rd);
+    const int P = plan_pages_per_split(a, lane);
+    const SplitRange sr = plan_locate(a, P, lane, 0, -1);
+    const int count = sr.b < 0 ? 0 : sr.count;
+#pragma unroll
+    for (int u = 0; u < kMergeMU; ++u) {
+      if (sg + u * SPI >= count) {
+        rd.ms[u] = -INFINITY;
+        rd.ls[u] = 0.f;
+        rd.os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    merge_fold_round(acc, rd);
+  } else {
+    const int P = plan_pages_per_split(a, lane);
+    const SplitRange sr = plan_locate(a, P, lane, mr.b, -1);
+    acc = merge_fold<D>(a, mr, col, sg, SPI, VPR, sr.first, sr.b < 0 ? 0 : sr.count);
+  }
   // The lanes of one column in a wave are col + VPR * j: combine them.
   float Mw = acc.M;
   for (int off = VPR; off < kWave; off <<= 1) Mw = fmaxf(Mw, __shfl_xor(Mw, off, kWave));
