@@ -310,9 +310,9 @@ struct MergeRound {
 };
 
 // Byte offsets of a unit's column inside one split state (layout written by
-// the split kernel: O [hkv][rows][D] fp16, then m and l [hkv][rows] fp32).
+// the split kernel: O [hkv][rows][D] fp16, then (m, l) [hkv][rows] fp32 pairs).
 struct MergeOffsets {
-  int64_t o, m, l;
+  int64_t o, ml;
 };
 template <int D>
 __device__ __forceinline__ MergeOffsets merge_offsets(const DecodeArgs &a, const MergeRow &mr, int col, int VPR) {
@@ -320,8 +320,7 @@ __device__ __forceinline__ MergeOffsets merge_offsets(const DecodeArgs &a, const
   const int dcol = 8 * (mr.slice * VPR + col);
   MergeOffsets o;
   o.o = (static_cast<int64_t>(mr.h * rows + mr.r) * D + dcol) * 2;
-  o.m = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 4;
-  o.l = o.m + a.hkv * rows * 4;
+  o.ml = static_cast<int64_t>(a.hkv) * rows * D * 2 + (mr.h * rows + mr.r) * 8;
   return o;
 }
 
@@ -335,8 +334,9 @@ __device__ __forceinline__ void merge_load(const DecodeArgs &a, const MergeOffse
     rd.os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (s < limit) {
       const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-      rd.ms[u] = *reinterpret_cast<const float *>(st + off.m);
-      rd.ls[u] = *reinterpret_cast<const float *>(st + off.l);
+      const float2 ml = *reinterpret_cast<const float2 *>(st + off.ml);
+      rd.ms[u] = ml.x;
+      rd.ls[u] = ml.y;
       rd.os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + off.o), v8f);
     }
   }
@@ -579,8 +579,10 @@ __device__ __forceinline__ void dma4s(const void *sbase, uint32_t voff, const ld
 __device__ __forceinline__ void store_wt16(void *dst, v8h v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
 }
-__device__ __forceinline__ void store_wt4(float *dst, float v) {
-  asm volatile("global_store_dword %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
+__device__ __forceinline__ void store_wt8(float2 *dst, float2 v) {
+  typedef float v2f_t __attribute__((ext_vector_type(2)));
+  const v2f_t x = {v.x, v.y};
+  asm volatile("global_store_dwordx2 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(x) : "memory");
 }
 
 // Per-lane byte offsets of one chunk's DMA sources (loop-invariant).
@@ -1567,20 +1569,21 @@ void decode_split_kernel(DecodeArgs a) {
 
   // Split state: O normalized by the split's row sum, times 1/4, in fp16
   // (lane rows 16nt+4g+i, dims dg*128+8n+j: one 16-byte store per row and
-  // dim group), then m and l in fp32.  A dequantized V value is at most
+  // dim group), then (m, l) in fp32.  A dequantized V value is at most
   // 15 * (65504 * 2 / 15) in magnitude, so a quarter of any average of them
-  // is a finite fp16; the merge multiplies by 4 again (exact).
+  // is a finite fp16; the merge multiplies by 4 again (exact).  m and l of a
+  // row go together (one 8-byte load per split in the merge).
   // (PH: each half writes its 128 dims of head hq's rows; m and l once.)
   constexpr int DQ = CFG::DQ, QH = CFG::QHEADS;
   char *base = a.ws + static_cast<int64_t>(role) * a.split_bytes;
   _Float16 *obase = reinterpret_cast<_Float16 *>(base);
-  float *mbase = reinterpret_cast<float *>(base + static_cast<int64_t>(QH) * rows * DQ * 2);
-  float *lbase = mbase + QH * rows;
+  float2 *mlbase = reinterpret_cast<float2 *>(base + static_cast<int64_t>(QH) * rows * DQ * 2);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = r0 + 16 * nt + 4 * g + i;
+      const float m_r = __shfl(st.m_run[nt], 4 * g + i, kWave);  // row r's max sits in lane n = 4 g + i
       if (r < rows) {
         const float l = st.lsum[nt][i];
         const float f = l > 0.f ? 0.25f / l : 0.f;
@@ -1593,11 +1596,9 @@ void decode_split_kernel(DecodeArgs a) {
                          static_cast<_Float16>(st.O[nt][dg][6][i] * f), static_cast<_Float16>(st.O[nt][dg][7][i] * f)};
           store_wt16(dst, o);
         }
-        if (n == 0 && half == 0) store_wt4(lbase + hq * rows + r, l);
+        if (n == 0 && half == 0) store_wt8(mlbase + hq * rows + r, make_float2(m_r, l));
       }
     }
-    const int r = r0 + 16 * nt + n;
-    if (g == 0 && half == 0 && r < rows) store_wt4(mbase + hq * rows + r, st.m_run[nt]);
   }
 }
 
@@ -1652,7 +1653,7 @@ int64_t query_tile_bytes(int64_t batch, int hkv, int head_dim) {
   return ((rows * head_dim + 255) / 256) * 256 + ((rows * 4 + 255) / 256) * 256;
 }
 
-// One split's state: per KV head and query row, D fp16 outputs, then m and l.
+// One split's state: per KV head and query row, D fp16 outputs, then (m, l).
 int64_t split_state_bytes(int hkv, int q_len, int head_dim) {
   return static_cast<int64_t>(hkv) * q_len * kGqa * (2 * head_dim + 8);
 }
