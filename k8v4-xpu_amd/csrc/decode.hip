@@ -1037,7 +1037,10 @@ struct SplitConfig {
   static constexpr int Q_TOTAL = QHEADS * Q_BYTES_PER_HEAD;
   // PH handshake words: per wave, the chunks whose K half is resident and
   // the chunks whose K slots it has finished reading.
-  static constexpr int FLAG_BYTES = PH ? 2 * WAVES * 4 : 0;
+  // Progress balance (two waves per head, eight waves: waves w and w + 4
+  // share a SIMD): one chunk counter per wave.
+  static constexpr bool BALANCE = NWH == 2 && WAVES == 8 && !PH;
+  static constexpr int FLAG_BYTES = PH ? 2 * WAVES * 4 : (BALANCE ? WAVES * 4 : 0);
   // One wave per SIMD (NWH == 1) has no partner wave to cover the table
   // lookup of a mid-chunk refill: it refills its K slot after P.V, next to
   // the V slot.  So does a PH wave, whose slot the other half of its pair
@@ -1434,8 +1437,24 @@ void decode_split_kernel(DecodeArgs a) {
       for (int j = 0; j < 8; ++j) st.O[nt][dg][j] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
 
+  // Two waves of one head share a SIMD (waves w and w + 4), and the SIMD
+  // favours the older one: left alone, the first wave of each head ends its
+  // loop about 15 us before the second at 4 x 131,072 tokens, which then runs
+  // alone.  Each wave publishes its chunk count and yields issue priority
+  // while it is ahead of its SIMD partner (90.4 -> 87.3 us there).  The
+  // paired halves are coupled per chunk already and run worse with it.
+  lds_int *prog = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);
+  if constexpr (CFG::BALANCE) pair_flag_set(prog + wave, 0, lane);
   for (int k = 0; k < cnt; ++k) {
     const int sk = k % RK, sv = k % RV;  // wave-uniform ring slots
+    if constexpr (CFG::BALANCE) {
+      pair_flag_set(prog + wave, k, lane);
+      const int pk = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const volatile lds_int *>(prog + (wave ^ 4)));
+      if (k > pk)
+        __builtin_amdgcn_s_setprio(0);
+      else
+        __builtin_amdgcn_s_setprio(1);
+    }
     lds_t *kslot = kring + sk * S::K_BYTES;
     lds_t *vslot = vring + sv * S::V_BYTES;
     int mks = mk[0], mvs = mv[0];
