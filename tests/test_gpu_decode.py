@@ -312,13 +312,15 @@ def test_explicit_visible_ends_out_of_order(gpu_ops):
     assert_close(out.cpu().numpy(), _oracle(cache, q, table, seq, q_len, visible=vis), what="explicit ends")
 
 
-def test_zero_length_rows_and_output_dtypes(gpu_ops):
-    lay = PageLayout(4, 128)
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+def test_zero_length_rows_and_output_dtypes(gpu_ops, hkv, d):
+    print("zero-length rows hkv=%d d=%d" % (hkv, d), flush=True)
+    lay = PageLayout(hkv, d)
     cache = Cache(8, lay)
     gen = torch.Generator().manual_seed(12)
     table = torch.tensor([[0, 1, 2], [3, 4, 5]], dtype=torch.int32)
     fill_sequence(gpu_ops, cache, gen, table[1], 150)
-    q = seeded_normal(gen, (2 * 3, 24, 128))
+    q = seeded_normal(gen, (2 * 3, 6 * hkv, d))
     seq = torch.tensor([0, 150])
     out16 = decode(gpu_ops, cache, q, table, seq, 3)
     assert bool((out16[:3] == 0).all())
