@@ -825,7 +825,7 @@ __device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target) {
 
 // Softmax and P.V of one chunk whose scores chunk_qk produced; reads the V
 // rows and scale planes of the chunk's V slot.
-template <int D, int NT, bool QLDS>
+template <int D, int NT, bool QLDS, bool RAISE = false>
 __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, const v4i (&sc)[2][NT],
                                                  const lds_t *vslot, int tbase, int L0, int lane, int g,
                                                  bool masked, const __attribute__((address_space(3))) int *lims) {
@@ -834,6 +834,12 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
   // Phase fences keep the scheduler from hoisting later LDS reads into this
   // phase, which would raise register pressure past two waves per SIMD.
   __builtin_amdgcn_sched_barrier(0);
+  // RAISE (the paired halves): the softmax's vector work runs at a raised
+  // issue priority, so beside the other wave's matrix phases it overlaps them
+  // instead of queueing behind that wave's vector instructions (reference
+  // shape 40.6 -> 40.2 us; with the 128-dim kernels' progress balance it
+  // measured slower at the headline, so they do not raise).
+  if constexpr (RAISE) __builtin_amdgcn_s_setprio(1);
   // ---- scale planes of this lane's 8 tokens: [0..3] = tokens 4g+i, [4..7] = 16+4g+i
   typedef float v4f_l __attribute__((ext_vector_type(4)));
   const auto *sp = reinterpret_cast<const __attribute__((address_space(3))) v4f_l *>(vslot + S::S_OFF);
@@ -952,6 +958,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
     st.corr[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PA[nt], bz, st.corr[nt], 0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (RAISE) __builtin_amdgcn_s_setprio(0);
   // ---- V: the packed bytes themselves are the B operand, read as fp16
   // subnormals: a byte in the low half of a 16-bit lane is (16 hi + lo) * 2^-24
   // and (x & 0x00F000F0) is hi * 2^-20.  Exact; the finalization takes the
@@ -1504,7 +1511,8 @@ void decode_split_kernel(DecodeArgs a) {
       for (int s = 0; s < RK; ++s)
         if (sk == s) mk[s] = issued;
     }
-    if (valid) chunk_softmax_pv<D, NT, CFG::QLDS>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end, lims);
+    if (valid)
+      chunk_softmax_pv<D, NT, CFG::QLDS, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end, lims);
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs);
       // PH: so have the other half's.
