@@ -46,9 +46,23 @@ __global__ __launch_bounds__(256) void q_quant_kernel(QQuantArgs a) {
     src = a.q + (static_cast<int64_t>(b) * a.q_len + tok) * a.tok_stride +
           static_cast<int64_t>(h * kGqa + (r - tok * kGqa)) * D;
   }
+  // One load per lane (rows start 16-byte aligned: both entry points require
+  // it), under one condition: per-element selects become one branch and
+  // one round trip each.
+  uint32_t words[E / 2] = {};
+  if (src) {
+    if constexpr (E == 4) {
+      const uint2 w = *reinterpret_cast<const uint2 *>(src + lane * E);
+      words[0] = w.x;
+      words[E / 2 - 1] = w.y;
+    } else {
+      words[0] = *reinterpret_cast<const uint32_t *>(src + lane * E);
+    }
+  }
   float x[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = src ? half_bits_to_float(src[lane * E + e], a.bf16) : 0.f;
+  for (int e = 0; e < E; ++e)
+    x[e] = half_bits_to_float(static_cast<uint16_t>(words[e >> 1] >> (16 * (e & 1))), a.bf16);
   float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(x[e]));
