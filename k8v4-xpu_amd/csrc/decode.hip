@@ -326,19 +326,26 @@ __device__ __forceinline__ MergeOffsets merge_offsets(const DecodeArgs &a, const
 
 __device__ __forceinline__ void merge_load(const DecodeArgs &a, const MergeOffsets &off, const char *ws, int s0,
                                            int SPI, int limit, MergeRound &rd) {
+  // All loads are issued before any is used: a split past `limit` reads the
+  // state of split limit - 1 (a live one) and is masked afterwards, so no
+  // load sits behind a per-split branch that would wait for it.
+  const bool any = s0 < limit;
+  v8h raw[kMergeMU] = {};
+  float2 ml[kMergeMU] = {};
+  if (any) {
+#pragma unroll
+    for (int u = 0; u < kMergeMU; ++u) {
+      const char *st = ws + static_cast<int64_t>(min(s0 + u * SPI, limit - 1)) * a.split_bytes;
+      ml[u] = *reinterpret_cast<const float2 *>(st + off.ml);
+      raw[u] = *reinterpret_cast<const v8h *>(st + off.o);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < kMergeMU; ++u) {
-    const int s = s0 + u * SPI;
-    rd.ms[u] = -INFINITY;
-    rd.ls[u] = 0.f;
-    rd.os[u] = (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (s < limit) {
-      const char *st = ws + static_cast<int64_t>(s) * a.split_bytes;
-      const float2 ml = *reinterpret_cast<const float2 *>(st + off.ml);
-      rd.ms[u] = ml.x;
-      rd.ls[u] = ml.y;
-      rd.os[u] = __builtin_convertvector(*reinterpret_cast<const v8h *>(st + off.o), v8f);
-    }
+    const bool live = s0 + u * SPI < limit;
+    rd.ms[u] = live ? ml[u].x : -INFINITY;
+    rd.ls[u] = live ? ml[u].y : 0.f;
+    rd.os[u] = live ? __builtin_convertvector(raw[u], v8f) : (v8f){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   }
 }
 
