@@ -241,6 +241,24 @@ __device__ SplitPlan plan_split(const DecodeArgs &a, int lane, int wg) {
   return sp;
 }
 
+// The merge's view of the plan: the split range of sequence want_b, in one
+// pass over the lengths when the batch fits one wave (one round trip, not
+// one for the pages per split and another for the scan).
+__device__ SplitRange plan_sequence(const DecodeArgs &a, int lane, int want_b) {
+  if (a.batch > kWave) return plan_locate(a, plan_pages_per_split(a, lane), lane, want_b, -1);
+  const int n = lane < a.batch ? seq_pages(a, lane) : 0;
+  const int total = wave_sum(n), maxn = wave_max(n);
+  int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
+  P = __builtin_amdgcn_readfirstlane(max(max(P, a.min_pages), 1));
+  const int s = (n + P - 1) / P;
+  const int excl = wave_inclusive_scan(s, lane) - s;
+  SplitRange r;
+  r.b = want_b;
+  r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, want_b, kWave));
+  r.count = __builtin_amdgcn_readfirstlane(__shfl(s, want_b, kWave));
+  return r;
+}
+
 // Block-table reads go through the constant address space: the table is
 // read-only for the kernel's lifetime, so a uniform lookup becomes a scalar
 // load and never waits on the vector-memory counter the LDS DMA uses.
@@ -410,8 +428,7 @@ __global__ __launch_bounds__(TPU) void decode_merge_kernel(DecodeArgs a) {
     // past the plan's count (stale states) are dropped afterwards.
     MergeRound rd;
     merge_load(a, merge_offsets<D>(a, mr, col, VPR), a.ws, sg, SPI, a.grid, rd);
-    const int P = plan_pages_per_split(a, lane);
-    const SplitRange sr = plan_locate(a, P, lane, 0, -1);
+    const SplitRange sr = plan_sequence(a, lane, 0);
     const int count = sr.b < 0 ? 0 : sr.count;
 #pragma unroll
     for (int u = 0; u < kMergeMU; ++u) {
@@ -423,8 +440,7 @@ __global__ __launch_bounds__(TPU) void decode_merge_kernel(DecodeArgs a) {
     }
     merge_fold_round(acc, rd);
   } else {
-    const int P = plan_pages_per_split(a, lane);
-    const SplitRange sr = plan_locate(a, P, lane, mr.b, -1);
+    const SplitRange sr = plan_sequence(a, lane, mr.b);
     acc = merge_fold<D>(a, mr, col, sg, SPI, VPR, sr.first, sr.b < 0 ? 0 : sr.count);
   }
   // The lanes of one column in a wave are col + VPR * j: combine them.
