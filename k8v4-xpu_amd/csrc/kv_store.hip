@@ -48,27 +48,29 @@ struct StoreArgs {
 
 constexpr int kStoreK = 1, kStoreV = 2;
 
-// E consecutive fp16/bf16 values -> fp32.
+// E consecutive fp16/bf16 values as E / 2 words (element 2i in the low
+// half of word i).  The conversion is a separate step so that the K and V
+// loads are all in flight before either is used.
 template <int E>
-__device__ __forceinline__ void load_row(const uint16_t *src, bool vec_ok, bool bf16, float out[E]) {
-  uint16_t h[E];
+__device__ __forceinline__ void load_words(const uint16_t *src, bool vec_ok, uint32_t w[E / 2]) {
   if (vec_ok) {
 #pragma unroll
     for (int c = 0; c < E / 8; ++c) {
-      const uint4 w = *reinterpret_cast<const uint4 *>(src + 8 * c);
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        h[8 * c + 2 * i] = static_cast<uint16_t>(words[i] & 0xFFFFu);
-        h[8 * c + 2 * i + 1] = static_cast<uint16_t>(words[i] >> 16);
-      }
+      const uint4 v = *reinterpret_cast<const uint4 *>(src + 8 * c);
+      w[4 * c] = v.x;
+      w[4 * c + 1] = v.y;
+      w[4 * c + 2] = v.z;
+      w[4 * c + 3] = v.w;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < E; ++i) h[i] = src[i];
+    for (int i = 0; i < E / 2; ++i) w[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
   }
+}
+template <int E>
+__device__ __forceinline__ void words_to_float(const uint32_t w[E / 2], bool bf16, float out[E]) {
 #pragma unroll
-  for (int i = 0; i < E; ++i) out[i] = half_bits_to_float(h[i], bf16);
+  for (int i = 0; i < E; ++i) out[i] = half_bits_to_float(static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1))), bf16);
 }
 
 // Max / min over the LPU lanes of one (token, head) group.
@@ -104,9 +106,12 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
   // The slot first: its load then shares the round trip of the K/V loads.
   const int64_t slot = a.slots[token];
   const bool do_k = a.parts & kStoreK, do_v = a.parts & kStoreV;  // uniform over the launch
+  uint32_t kwd[E / 2] = {}, vwd[E / 2] = {};
+  if (do_k) load_words<E>(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, kwd);
+  if (do_v) load_words<E>(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, vwd);
   float kx[E], vx[E];
-  if (do_k) load_row<E>(a.k + token * a.k_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, kx);
-  if (do_v) load_row<E>(a.v + token * a.v_tok_stride + static_cast<int64_t>(head) * D + E * sub, a.vec_ok, a.bf16, vx);
+  if (do_k) words_to_float<E>(kwd, a.bf16, kx);
+  if (do_v) words_to_float<E>(vwd, a.bf16, vx);
 
   float amax = 0.f, lo = 0.f, hi = 0.f;
   if (do_k) {
