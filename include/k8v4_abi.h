@@ -29,7 +29,13 @@
 extern "C" {
 #endif
 
-#define K8V4_ABI_VERSION 1
+/*
+ * Version 2: at head dim 256 with two KV heads the decode workspace holds the
+ * quantized query tile ahead of the split states, and
+ * k8v4_attn_workspace_bytes counts it (a workspace sized as splits x state
+ * bytes alone now holds fewer splits).  Version 1: the first release.
+ */
+#define K8V4_ABI_VERSION 2
 
 enum {
   K8V4_OK = 0,
@@ -208,7 +214,8 @@ int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const i
  * k8v4_attn_batch without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * split states go to a library-owned device buffer of
+ * split states (and, at head dim 256 with two KV heads, the quantized query
+ * tile ahead of them) go to a library-owned device buffer of
  * k8v4_attn_noalloc_max_bytes() bytes (32 MiB) per GPU, held until the
  * process ends; a call whose k8v4_attn_workspace_bytes exceeds it returns
  * K8V4_ERR_WORKSPACE without launching anything.  The call allocates nothing
@@ -226,8 +233,18 @@ int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok_stride, co
                             int hkv, int head_dim, void *out, int out_dtype, int64_t out_tok_stride,
                             int num_splits, void *stream);
 
-/* Bytes of the library-owned split-state buffer of k8v4_attn_batch_noalloc. */
+/* Bytes of the library-owned buffer of k8v4_attn_batch_noalloc (split states
+ * and, at head dim 256 with two KV heads, the query tile). */
 int64_t k8v4_attn_noalloc_max_bytes(void);
+
+/*
+ * Diagnostics, no counterpart in the reference: how many in-kernel waits of
+ * the decode kernels on the current device gave up since the library was
+ * loaded (the paired-halves handshake of head dim 256 with two KV heads caps
+ * each wait; a give-up means a wrong output).  Synchronizes with the device
+ * (a copy from device memory); -1 on a HIP error.  Zero in a correct run.
+ */
+int64_t k8v4_decode_fault_count(void);
 
 /* Workspace bytes k8v4_prefill_paged needs (0 for q_len == 0, -1 on bad
  * arguments).  No counterpart in the reference (its prefill allocated its

@@ -833,17 +833,21 @@ __device__ __forceinline__ void chunk_qk_pair(const lds_t *klo, const lds_t *khi
 // until it reaches the target, sleeping between polls.  The pair runs the
 // same chunk sequence and neither wave waits before publishing what the
 // other waits for, so every wait ends; the bound only caps a wait that a
-// broken launch could otherwise make endless.
+// broken launch could otherwise make endless, and such a give-up is counted
+// in a device word the host reads (k8v4_decode_fault_count), so it shows up
+// in tests instead of as a silently wrong output.
 typedef __attribute__((address_space(3))) int lds_int;
+__device__ int g_pair_wait_timeouts;
 __device__ __forceinline__ void pair_flag_set(lds_int *f, int v, int lane) {
   if (lane == 0) *reinterpret_cast<volatile lds_int *>(f) = v;
 }
-__device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target) {
+__device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target, int lane) {
   for (int it = 0; it < (1 << 22); ++it) {
     const int v = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const volatile lds_int *>(f));
-    if (v >= target) break;
+    if (v >= target) return;
     __builtin_amdgcn_s_sleep(1);
   }
+  if (lane == 0) __hip_atomic_fetch_add(&g_pair_wait_timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Softmax and P.V of one chunk whose scores chunk_qk produced; reads the V
@@ -1223,13 +1227,19 @@ void decode_split_kernel(DecodeArgs a) {
   const bool tab_vgpr = p1 - p0 <= 128;
   int ptab[2] = {-1, -1};
   if (tab_vgpr) {
+    // Both entries are loaded before either is used (one round trip; a lane
+    // past the run reads the run's last entry and is dropped below).
+    int raw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = min(p0 + 64 * i + lane, p1 - 1);
+      raw[i] = bt_row[a.ppb <= 1 ? p : p / a.ppb];
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int p = p0 + 64 * i + lane;
-      if (p < p1) {
-        const int ph = a.ppb <= 1 ? bt_row[p] : bt_row[p / a.ppb] * a.ppb + p % a.ppb;
-        ptab[i] = (ph >= 0 && ph < a.num_pages) ? ph : -1;
-      }
+      const int ph = a.ppb <= 1 ? raw[i] : raw[i] * a.ppb + p % a.ppb;
+      ptab[i] = (p < p1 && ph >= 0 && ph < a.num_pages) ? ph : -1;
     }
   }
   auto page_of = [&](int x) -> int {  // x: chunk index in the sequence (wave-uniform)
@@ -1506,7 +1516,7 @@ void decode_split_kernel(DecodeArgs a) {
     if constexpr (PH) {
       // This wave's half of chunk k is resident; wait for the other half.
       pair_flag_set(flags + wave, k + 1, lane);
-      pair_flag_wait(flags + (wave ^ 1), k + 1);
+      pair_flag_wait(flags + (wave ^ 1), k + 1, lane);
     }
     const bool valid = (valid_mask >> sk) & 1u;
     const int tbase = 32 * (my0 + k * NWH);
@@ -1539,7 +1549,7 @@ void decode_split_kernel(DecodeArgs a) {
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs);
       // PH: so have the other half's.
-      if constexpr (PH) pair_flag_wait(flags + CFG::WAVES + (wave ^ 1), k + 1);
+      if constexpr (PH) pair_flag_wait(flags + CFG::WAVES + (wave ^ 1), k + 1, lane);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
       int lane_o = lane;
@@ -1983,6 +1993,18 @@ int scratch_address(void **out) {
 
 extern "C" int64_t k8v4_attn_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
+extern "C" int64_t k8v4_decode_fault_count(void) {
+  using namespace k8v4;
+  clear_error();
+  int n = 0;
+  const hipError_t e = hipMemcpyFromSymbol(&n, HIP_SYMBOL(g_pair_wait_timeouts), sizeof(n));
+  if (e != hipSuccess) {
+    set_error("k8v4_decode_fault_count: %s", hipGetErrorString(e));
+    return -1;
+  }
+  return n;
+}
+
 extern "C" int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
                                        const float *k_scale, const uint8_t *v_cache, const float *v_scale,
                                        const float *v_zero, int64_t num_pages, int64_t k_page_stride,
@@ -1999,8 +2021,9 @@ extern "C" int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok
   K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
   K8V4_REQUIRE(need >= 0, "bad shape for the decode workspace");
   if (need > kNoAllocScratchBytes) {
-    set_error("k8v4_attn_batch_noalloc: the call needs %lld bytes of split states, the library-owned buffer "
-              "holds %lld (use k8v4_attn_batch with a caller workspace)",
+    set_error("k8v4_attn_batch_noalloc: the call needs %lld bytes of split states (and, at head dim 256 with "
+              "two KV heads, the quantized query tile), the library-owned buffer holds %lld (use "
+              "k8v4_attn_batch with a caller workspace)",
               static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
     return K8V4_ERR_WORKSPACE;
   }

@@ -159,7 +159,7 @@ class Xe2K8V4MetadataBuilder(AttentionMetadataBuilder[Xe2K8V4Metadata]):
             list(capture),
             self.layout,
         )
-        return ensure_scratch(self.device, self.layout, *capacity)
+        return ensure_scratch(self.device, self.layout, *capacity, max_seqs=int(cfg.scheduler_config.max_num_seqs))
 
     def build(
         self,

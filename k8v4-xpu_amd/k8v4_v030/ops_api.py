@@ -88,6 +88,7 @@ _EXTRA_SYMBOLS.append((
 ))
 _EXTRA_SYMBOLS.append(("k8v4_attn_batch_noalloc", _EXTRA_SYMBOLS[0][1][:28] + [_i32, _vp], _i32))
 _EXTRA_SYMBOLS.append(("k8v4_attn_noalloc_max_bytes", [], _i64))
+_EXTRA_SYMBOLS.append(("k8v4_decode_fault_count", [], _i64))
 Q_TOKENS, Q_PADDED = 0, 1
 
 

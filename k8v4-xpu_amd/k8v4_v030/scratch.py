@@ -37,12 +37,18 @@ def _library_ops():
     return ops()
 
 
-def decode_workspace_bytes(layout: PageLayout, max_pages: int, max_out_tokens: int) -> int:
-    """Largest decode workspace over every query length 1..10 at ``max_out_tokens`` query rows."""
+def decode_workspace_bytes(layout: PageLayout, max_pages: int, max_out_tokens: int,
+                           max_seqs: int | None = None) -> int:
+    """Largest decode workspace over every query length 1..10 at ``max_out_tokens``
+    query rows, for at most ``max_seqs`` sequences per call (when given: a
+    decode call never holds more sequences than the engine schedules, however
+    many query rows the output buffer allows)."""
     lib = _library_ops()
     need = 0
     for q_len in range(1, DECODE_MAX_T + 1):
         batch = max(1, int(max_out_tokens) // q_len)
+        if max_seqs is not None:
+            batch = max(1, min(batch, int(max_seqs)))
         need = max(need, lib.attn_workspace_bytes(batch, int(max_pages), 1, q_len, layout.hkv, layout.head_dim))
     return need
 
@@ -64,16 +70,20 @@ class Scratch:
         nprog_max: int,
         max_store_tokens: int,
         max_out_tokens: int,
+        max_seqs: int | None = None,
     ):
         if min(int(nprog_max), int(max_store_tokens), int(max_out_tokens)) < 1:
+            raise ValueError("scratch capacity")
+        if max_seqs is not None and int(max_seqs) < 1:
             raise ValueError("scratch capacity")
         self.device = torch.device(device)
         self.layout = layout
         self.nprog_max = int(nprog_max)
         self.max_store_tokens = int(max_store_tokens)
         self.max_out_tokens = int(max_out_tokens)
+        self.max_seqs = None if max_seqs is None else int(max_seqs)
         self.max_pages = -(-self.nprog_max // layout.hkv)
-        self.decode_bytes = decode_workspace_bytes(layout, self.max_pages, self.max_out_tokens)
+        self.decode_bytes = decode_workspace_bytes(layout, self.max_pages, self.max_out_tokens, self.max_seqs)
         self.prefill_bytes = prefill_workspace_bytes(layout, self.max_pages, self.max_store_tokens)
         self.decode_ws = torch.empty(_words(self.decode_bytes), dtype=torch.int32, device=self.device)
         self.prefill_ws = torch.empty(_words(self.prefill_bytes), dtype=torch.int32, device=self.device)
@@ -130,9 +140,10 @@ class Scratch:
         shape = (self.max_out_tokens, self.layout.hq, self.layout.head_dim)
         return self._lazy("q16", shape, torch.float16)[:n], self._lazy("o16", shape, torch.float16)[:n]
 
-    def covers(self, nprog_max: int, max_store_tokens: int, max_out_tokens: int) -> bool:
+    def covers(self, nprog_max: int, max_store_tokens: int, max_out_tokens: int, max_seqs: int | None = None) -> bool:
+        seqs_ok = self.max_seqs is None or (max_seqs is not None and self.max_seqs >= int(max_seqs))
         return (self.nprog_max >= int(nprog_max) and self.max_store_tokens >= int(max_store_tokens)
-                and self.max_out_tokens >= int(max_out_tokens))
+                and self.max_out_tokens >= int(max_out_tokens) and seqs_ok)
 
 
 def _words(nbytes: int) -> int:
@@ -149,16 +160,24 @@ def scratch_key(device: torch.device, layout: PageLayout) -> tuple[str, int | No
     return device.type, index, layout.hkv, layout.head_dim
 
 
-def ensure_scratch(device, layout: PageLayout, nprog_max: int, max_store_tokens: int, max_out_tokens: int) -> Scratch:
-    """The registered scratch of (device, layout), replaced by a larger one when it is too small."""
+def ensure_scratch(device, layout: PageLayout, nprog_max: int, max_store_tokens: int, max_out_tokens: int,
+                   max_seqs: int | None = None) -> Scratch:
+    """The registered scratch of (device, layout), replaced by a larger one when it is too small.
+
+    ``max_seqs`` (optional) caps the sequences of one decode call; without it
+    the decode workspace covers ``max_out_tokens`` one-token sequences."""
     key = scratch_key(device, layout)
     have = _REGISTRY.get(key)
-    if have is None or not have.covers(nprog_max, max_store_tokens, max_out_tokens):
+    if have is None or not have.covers(nprog_max, max_store_tokens, max_out_tokens, max_seqs):
         if have is not None:
             nprog_max = max(int(nprog_max), have.nprog_max)
             max_store_tokens = max(int(max_store_tokens), have.max_store_tokens)
             max_out_tokens = max(int(max_out_tokens), have.max_out_tokens)
-        have = _REGISTRY[key] = Scratch(device, layout, nprog_max, max_store_tokens, max_out_tokens)
+            if max_seqs is not None and have.max_seqs is not None:
+                max_seqs = max(int(max_seqs), have.max_seqs)
+            else:
+                max_seqs = None
+        have = _REGISTRY[key] = Scratch(device, layout, nprog_max, max_store_tokens, max_out_tokens, max_seqs)
     return have
 
 

@@ -48,7 +48,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
         assert fn is not None
         if name in bound:
             assert len(bound[name]) == nparams, name
-    assert lib.k8v4_abi_version() == 1
+    assert lib.k8v4_abi_version() == 2
 
 
 def _attn(lib, **over):

@@ -165,10 +165,15 @@ def test_scratch_covers_every_decode_call_the_engine_can_issue(hkv, head, max_mo
     s = get_scratch(torch.device("cpu"), b.layout)
     lib = ops()
     pages = -(-max_model_len // 64) + 1
+    max_out = max(max_seqs * 10, 16)
+    sized = 0
     for q_len in range(1, 11):
         batch = max_seqs
         need = lib.attn_workspace_bytes(batch, pages, 1, q_len, hkv, head)
         assert s.decode_ws.numel() * 4 >= need, (q_len, need)
+        sized = max(sized, lib.attn_workspace_bytes(min(max_seqs, max_out // q_len), pages, 1, q_len, hkv, head))
+    # No larger than that: a call never holds more sequences than the engine schedules.
+    assert s.decode_bytes == sized and s.max_seqs == max_seqs
     assert s.prefill_ws.numel() * 4 >= lib.prefill_workspace_bytes(min(max_batched, pages * 64), min(max_batched, pages * 64), hkv, head)
     # Tens of MB per device, not the reference's [pages x heads, 64, D] fp32 partials.
     assert s.nbytes < 200 * 2 ** 20

@@ -467,3 +467,13 @@ def test_bound_call_and_stages_match_the_plain_op(gpu_ops):
     assert max_abs(out, again) == 0.0
     with pytest.raises(RuntimeError, match="stages"):
         call(stages=0)
+
+
+def test_no_in_kernel_wait_gave_up(gpu_ops):
+    """Every paired-halves handshake of the decode runs above ended normally
+    (a capped wait that gives up is counted on the device, and would mean a
+    wrong output)."""
+    from k8v4_v030 import ops_api
+
+    torch.cuda.synchronize()
+    assert ops_api.load_library().k8v4_decode_fault_count() == 0

@@ -43,25 +43,28 @@ def _both(lib, cache, q, table, seq, q_len):
     return with_ws, no_ws
 
 
-def test_noalloc_entry_matches_the_workspace_entry_on_two_calls():
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+def test_noalloc_entry_matches_the_workspace_entry_on_two_calls(hkv, d):
+    """(4, 128): split states only; (2, 256): the paired-halves layout, whose
+    query tile sits ahead of the split states in the same buffer."""
     lib = ops_api.load_library()
-    print("noalloc: first call (4 x 20,000, q=7)", flush=True)
-    lay = PageLayout(4, 128)
-    gen = torch.Generator().manual_seed(777)
-    lengths = [20000, 20000, 15000, 9000]
-    table = random_tables(gen, lengths, 1300)
-    cache = Cache(1300, lay)
+    print("noalloc hkv=%d d=%d: first call (2 x 20,000, q=7)" % (hkv, d), flush=True)
+    lay = PageLayout(hkv, d)
+    gen = torch.Generator().manual_seed(777 + d)
+    lengths = [20000, 17000]
+    table = random_tables(gen, lengths, 700)
+    cache = Cache(700, lay)
     for b, L in enumerate(lengths):
         fill_sequence(ops_api.ops(), cache, gen, table[b], L)
-    q = seeded_normal(gen, (4 * 7, 24, 128)).to(DEV)
+    q = seeded_normal(gen, (2 * 7, lay.hq, d)).to(DEV)
     tbl = table.to(DEV)
     seq = torch.tensor(lengths, dtype=torch.int32, device=DEV)
     a, b = _both(lib, cache, q, tbl, seq, 7)
     assert torch.isfinite(a).all() and torch.equal(a, b)
-    print("noalloc: second call (2 x 3,000, q=3)", flush=True)
-    q2 = seeded_normal(gen, (2 * 3, 24, 128)).to(DEV)
-    seq2 = torch.tensor([3000, 2500], dtype=torch.int32, device=DEV)
-    a2, b2 = _both(lib, cache, q2, tbl[:2].contiguous(), seq2, 3)
+    print("noalloc hkv=%d d=%d: second call (1 x 3,000, q=3)" % (hkv, d), flush=True)
+    q2 = seeded_normal(gen, (1 * 3, lay.hq, d)).to(DEV)
+    seq2 = torch.tensor([3000], dtype=torch.int32, device=DEV)
+    a2, b2 = _both(lib, cache, q2, tbl[:1].contiguous(), seq2, 3)
     assert torch.isfinite(a2).all() and torch.equal(a2, b2)
 
 
