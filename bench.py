@@ -15,8 +15,8 @@ non-contiguous block tables.  Prints ONE JSON line:
   rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
 * ``cpu_baseline``: the reference's PyTorch path restated in torch
   (oracle/torch_cpu.py) on every host core: the whole headline decode step,
-  config 2's store and a sample of config 5's prefill; the float64 oracle
-  checks the GPU's headline output;
+  config 2's store and config 5's whole prefill chunk; the float64 oracle
+  checks the GPU's headline output, the torch port the GPU's prefill output;
 * ``step_graph_us`` and the configs' ``graph_us_*``: per-launch time from HIP
   graphs of back-to-back launches replayed between two events (median and
   min of several replays), which leaves out the host launch cost;
@@ -60,6 +60,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default=None,
                     help="run only the config rows whose name contains this text (no headline; for profiling)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="with --only: also time the 1 GiB device copy that calibrates the byte counters")
     return ap.parse_args(argv)
 
 
@@ -151,7 +153,12 @@ class DecodeWorkload:
         nbytes = ops.attn_workspace_bytes(self.batch, self.width, 1, q_len, hkv, head_dim, splits)
         self.ws = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
         self.splits = splits
+        # Bytes the step reads (a shared prefix page once per sequence that reads it),
+        # and the distinct bytes behind them (each shared page counted once).
         self.kv_bytes = sum(self.lengths) * self.layout.bytes_per_token
+        shared_tokens = shared_prefix_pages * PAGE
+        self.unique_kv_bytes = (min(max(self.lengths), shared_tokens)
+                                + sum(max(0, n - shared_tokens) for n in self.lengths)) * self.layout.bytes_per_token
         v = self.views
         self.calls = [
             ops.bind_int8k_int4v_attn_batch(
@@ -388,8 +395,8 @@ def cpu_baseline(torch, work, store_work=None, prefill_work=None):
 
     decode: the whole headline step (4 x 131,072 tokens, q = 7) -- gather and
     dequantize, int8 query rows, fp32 attention; store: config 2's 16,896 tokens
-    quantized into the cache; prefill: the last rows of config 5's chunk over all
-    135,296 keys (key-tiled online softmax).  Median of 3 after one warm-up.
+    quantized into the cache (both median of 3 after one warm-up); prefill:
+    config 5's whole chunk over all 135,296 keys (key-tiled online softmax), once.
     The float64 oracle checks the GPU's headline output on the same cache."""
     import numpy as np
 
@@ -455,22 +462,28 @@ def cpu_store_baseline(torch, w, torch_cpu, geom):
                       % w.ntok}
 
 
-def cpu_prefill_baseline(torch, w, torch_cpu, rows=512):
-    """The last ``rows`` query tokens of config 5's chunk over all its keys, on the host."""
+def cpu_prefill_baseline(torch, w, torch_cpu):
+    """Config 5's whole chunk (4,224 query tokens over all 135,296 keys) on the
+    host, once (about 17 s on 16 cores); the GPU's output of the same chunk is
+    compared with it."""
     from oracle import paged
 
     geom = paged.Geometry(w.layout.hkv, w.layout.head_dim)
     raw = w.raw.view(torch.uint8).cpu()
     views = torch_cpu.region_views(raw, geom)
-    q = w.q[-rows:].cpu()
+    q = w.q.cpu()
     row = w.row.cpu()
-    sec = median_seconds(lambda: torch_cpu.prefill(views, q, row, w.seq_len, 1.0 / math.sqrt(w.layout.head_dim)))
-    pairs = rows * (w.seq_len - rows) + rows * (rows + 1) // 2
-    flops = pairs * 6 * w.layout.hkv * 4 * w.layout.head_dim
-    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "seconds": round(sec, 3),
-            "full_chunk_us_estimate": round(sec * w.flops / flops * 1e6, 0),
-            "sample": "last %d of the %d query tokens over all %d keys (key tiles of 16,384, row groups of 256, "
-                      "fp32)" % (rows, w.q_len, w.seq_len)}
+    w.launch(0)
+    torch.cuda.synchronize()
+    gpu = w.out.float().cpu()
+    t0 = time.perf_counter()
+    want = torch_cpu.prefill(views, q, row, w.seq_len, 1.0 / math.sqrt(w.layout.head_dim))
+    sec = time.perf_counter() - t0
+    return {"value": round(w.flops / sec / 1e12, 4), "unit": "TFLOP/s", "seconds": round(sec, 3),
+            "us_per_layer": round(sec * 1e6, 0),
+            "gpu_vs_cpu_port_max_abs_err": float((gpu - want).abs().max()),
+            "sample": "the whole chunk: %d query tokens over all %d keys, one run (key tiles of 16,384, row groups "
+                      "of 256, fp32)" % (w.q_len, w.seq_len)}
 
 
 # --------------------------------------------------------------------- configs
@@ -499,6 +512,14 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
             "pct_of_hbm_peak": round(100 * w.kv_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
             "cache_copies_rotated": copies,
         }
+        if w.unique_kv_bytes != w.kv_bytes:
+            # A shared prefix is read once per sequence in the same step: the rate
+            # on distinct bytes sits beside the rate on bytes read.
+            rows[name].update({
+                "unique_kv_bytes": w.unique_kv_bytes,
+                "GBps_unique": round(w.unique_kv_bytes / (us * 1e-6) / 1e9, 1),
+                "pct_of_hbm_peak_unique": round(100 * w.unique_kv_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+            })
         del w
         torch.cuda.empty_cache()
         progress("%s: %.2f us/layer" % (name, us))
@@ -566,7 +587,10 @@ def main(argv=None) -> int:
     hip = HipEvents()
     if args.only:
         rows = config_rows(torch, hip, o, min(args.steps, 100), min(args.warmup, 10), only=args.only)
-        print(json.dumps({"configs": rows}), flush=True)
+        line = {"configs": rows}
+        if args.calibrate_copy:
+            line["copy_peak_GBps"] = round(copy_peak_gbs(torch, hip), 1)
+        print(json.dumps(line), flush=True)
         return 0
     B, ctx, q_len = 4, 131072, 7
     work = DecodeWorkload(o, torch, lengths=[ctx] * B, q_len=q_len, hkv=4, head_dim=128, copies=3,
