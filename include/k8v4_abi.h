@@ -211,6 +211,39 @@ int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const i
                        void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
+ * k8v4_prefill_paged over several sequences at once: the prefill chunks of
+ * one engine step (replaces the reference's per-request loop in the
+ * backend, backend.py:376-409 calling dequant.py:213-242 once per request).
+ * Sequence i has q_lens[i] query rows at token tok0[i] of q and out (same
+ * layouts and strides as k8v4_prefill_paged, shared by all sequences),
+ * seq_lens[i] keys, and its block-table row at block_table + rows[i] *
+ * bt_stride (table_width entries of pages_per_block pages).  tok0, q_lens,
+ * seq_lens and rows are HOST arrays of nseq entries.  Per launch the kernels
+ * take up to 10 non-empty sequences, whose (KV head, row block) work shares
+ * the persistent work-groups of one launch; more sequences take more
+ * launches, in order, on the stream.  Pages are dequantized in the kernel
+ * (no per-head tile pre-pass), which suits short chunks: a long chunk is
+ * faster through k8v4_prefill_paged.  The same bottom-right causal rule,
+ * numerics and errors per sequence as k8v4_prefill_paged; q_lens[i] == 0
+ * sequences are skipped; nseq == 0 is a no-op.
+ * workspace: >= k8v4_prefill_batch_workspace_bytes(hkv, head_dim) bytes.
+ */
+int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                             const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                             const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                             int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                             int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                             int64_t table_width, int pages_per_block, int nseq, const int64_t *tok0,
+                             const int64_t *q_lens, const int64_t *seq_lens, const int64_t *rows, int hkv,
+                             int head_dim, float scale, void *out, int out_dtype, int64_t out_tok_stride,
+                             void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes k8v4_prefill_paged_batch needs (-1 on bad arguments):
+ * the partial states of one launch, whatever its sequences.  No counterpart
+ * in the reference. */
+int64_t k8v4_prefill_batch_workspace_bytes(int hkv, int head_dim);
+
+/*
  * k8v4_attn_batch without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The

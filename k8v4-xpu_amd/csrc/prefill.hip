@@ -1196,33 +1196,32 @@ __global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, cha
 // per row, D/2 dims each.
 constexpr int kMergeSplit = 4;
 
-template <int D>
-__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_merge_kernel(PrefillArgs a) {
-  constexpr int R = Tile<D>::ROWS;
-  const int b = blockIdx.x / kMergeSplit;
-  const int quarter = blockIdx.x % kMergeSplit;
-  const int hl = b / a.nbh, rb = b % a.nbh;
-  const int h = a.head0 + hl;
-  const int lane = threadIdx.x % 64;
-  int start = 0;
-  {
-    // steps before block rb of head h
-    int base = 0;
-    for (int r0 = 0; r0 < rb; r0 += 64) {
-      const int r = r0 + lane;
-      int n = r < rb ? block_pages(a, r) : 0;
+// Steps of row blocks 0 .. rb - 1 of one KV head (wave-uniform).
+__device__ __forceinline__ int steps_before_block(const PrefillArgs &a, int rb, int lane) {
+  int base = 0;
+  for (int r0 = 0; r0 < rb; r0 += 64) {
+    const int r = r0 + lane;
+    int n = r < rb ? block_pages(a, r) : 0;
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
-      base += n;
-    }
-    start = hl * a.tper + base;
+    for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
+    base += n;
   }
-  const int n = block_pages(a, rb);
+  return base;
+}
+
+// Merges row block rb of KV head h (one sequence's fields in `sa`) whose
+// steps start at `start` of the launch's step line, if work-groups split it;
+// `a` holds the launch's schedule (total, grid) and workspace.
+template <int D>
+__device__ __forceinline__ void merge_block(const PrefillArgs &a, const PrefillArgs &sa, int h, int rb, int start,
+                                            int quarter) {
+  constexpr int R = Tile<D>::ROWS;
+  const int n = block_pages(sa, rb);
   const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
   if (va == vb) return;  // one work-group did the whole block
   const int lr = quarter * (R / kMergeSplit) + threadIdx.x / 2, half = threadIdx.x % 2;
   const int row = rb * R + lr;
-  if (row >= a.q_len * 6) return;
+  if (row >= sa.q_len * 6) return;
   float M = -INFINITY;
   for (int v = va; v <= vb; ++v) {
     const int slot = range_start(a, v) >= start ? 0 : 1;
@@ -1246,9 +1245,114 @@ __global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_merge
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int tok = row / 6, qh = h * 6 + row % 6;
-  const int64_t ob = static_cast<int64_t>(tok) * a.out_tok_stride + static_cast<int64_t>(qh) * D + half * (D / 2);
+  const int64_t ob = static_cast<int64_t>(tok) * sa.out_tok_stride + static_cast<int64_t>(qh) * D + half * (D / 2);
 #pragma unroll
-  for (int e = 0; e < D / 8; ++e) store_out4(a.out, a.out_dtype, ob + 4 * e, o[e] * inv);
+  for (int e = 0; e < D / 8; ++e) store_out4(sa.out, sa.out_dtype, ob + 4 * e, o[e] * inv);
+}
+
+template <int D>
+__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_merge_kernel(PrefillArgs a) {
+  const int b = blockIdx.x / kMergeSplit;
+  const int hl = b / a.nbh, rb = b % a.nbh;
+  const int start = hl * a.tper + steps_before_block(a, rb, threadIdx.x % 64);
+  merge_block<D>(a, a, a.head0 + hl, rb, start, blockIdx.x % kMergeSplit);
+}
+
+// ---- several sequences in one launch (the short chunks of one step)
+// Their (KV head, row block) work is laid out sequence after sequence as one
+// line of page steps (each sequence head-major, as above) that the persistent
+// work-groups share out as for one sequence; blocks are numbered the same way
+// for the merge.  The kernel argument holds one complete PrefillArgs per
+// sequence (its rows of q and out, lengths, block-table row; the schedule
+// fields of the launch are in every one), and a segment reads its
+// sequence's through a reference into the kernel-argument segment at a
+// wave-uniform offset: scalar loads on demand, as the one-sequence kernels
+// read theirs (a copy in registers would not fit beside the kernels' own).
+constexpr int kBatchMax = 10;
+struct PrefillBatchArgs {
+  PrefillArgs seq[kBatchMax];  // must stay the first member: read at kernarg offset i * sizeof(PrefillArgs)
+  int n;                       // sequences of this launch
+  int step0[kBatchMax + 1];    // first page step of sequence i; step0[n] = the launch's total
+  int block0[kBatchMax + 1];   // first (KV head, row block) of sequence i; block0[n] = blocks of the launch
+};
+
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Sequence holding item x of an increasing prefix line off[0..n] (wave-uniform;
+// constant indices only: a runtime index into the by-value argument would copy
+// it to private memory).
+__device__ __forceinline__ int batch_find(const int (&off)[kBatchMax + 1], int n, int x) {
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kBatchMax; ++k)
+    if (k < n && off[k] <= x) i = k;
+  return uni(i);
+}
+__device__ __forceinline__ int batch_off(const int (&off)[kBatchMax + 1], int i) {
+  int v = off[0];
+#pragma unroll
+  for (int k = 1; k <= kBatchMax; ++k)
+    if (i == k) v = off[k];
+  return uni(v);
+}
+
+// Sequence i's arguments, in place in the kernel-argument segment.
+__device__ __forceinline__ const PrefillArgs &batch_seq(int i) {
+  typedef const __attribute__((address_space(4))) PrefillArgs const_args;
+  const_args *base = (const_args *)__builtin_amdgcn_kernarg_segment_ptr();
+  return *(const PrefillArgs *)(base + i);
+}
+
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(Tile<D>::THREADS, Tile<D>::THREADS),
+                          amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
+prefill_batch_kernel(PrefillBatchArgs ba) {
+  using T = Tile<D>;
+  constexpr int LDS_BYTES = D == 128 ? PP::LDS : 2 * T::BUF + T::STAGE;
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
+  const PrefillArgs &a = ba.seq[0];  // the launch's schedule
+  const int w = blockIdx.x;
+  const int v = a.xcd_perm ? (w % 8) * (a.grid / 8) + w / 8 : w;
+  const int s0 = range_start(a, v), s1 = range_start(a, v + 1);
+  if (s0 >= s1) return;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
+  if constexpr (D == 128) {
+    for (int o = 16 * tid; o < 4 * PP::BUF; o += 16 * PP::THREADS) *reinterpret_cast<uint4 *>(smem + o) = make_uint4(0, 0, 0, 0);
+  }
+  int s = s0;
+  bool first = true;
+  while (s < s1) {
+    const int i = batch_find(ba.step0, ba.n, s);
+    const PrefillArgs &sa = batch_seq(i);
+    const int sl = s - batch_off(ba.step0, i);  // step within the sequence
+    const int h = sl / sa.tper;
+    int rb, before;
+    locate_block(sa, sl - h * sa.tper, lane, rb, before);
+    const int n = block_pages(sa, rb);
+    const int p_lo = sl - h * sa.tper - before;
+    const int p_hi = min(n, p_lo + (s1 - s));
+    float *part = nullptr;
+    if (p_lo != 0 || p_hi != n) part = a.ws + (static_cast<int64_t>(v) * 2 + (first ? 0 : 1)) * T::ROWS * (D + 2);
+    if constexpr (D == 128)
+      run_segment_pp<false>(sa, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+    else
+      run_segment<D>(sa, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+    s += p_hi - p_lo;
+    first = false;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_batch_merge_kernel(PrefillBatchArgs ba) {
+  const int b = blockIdx.x / kMergeSplit;
+  const int i = batch_find(ba.block0, ba.n, b);
+  const PrefillArgs &sa = batch_seq(i);
+  const int local = b - batch_off(ba.block0, i);
+  const int h = local / sa.nbh, rb = local % sa.nbh;
+  const int start = batch_off(ba.step0, i) + h * sa.tper + steps_before_block(sa, rb, threadIdx.x % 64);
+  merge_block<D>(ba.seq[0], sa, h, rb, start, blockIdx.x % kMergeSplit);
 }
 
 }  // namespace
@@ -1301,6 +1405,66 @@ int64_t workspace_need(const PrefillPlan &pl, int64_t seq_len, int head_dim) {
   return tiles_offset(pl, head_dim) + (seq_len + kPage - 1) / kPage * PP::BUF;
 }
 
+
+// Argument checks shared by the single-sequence and batched prefill entries.
+int check_prefill_args(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache, const float *k_scale,
+                       const uint8_t *v_cache, const float *v_scale, const float *v_zero, int64_t k_page_stride,
+                       int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                       int64_t vz_page_stride, const int32_t *block_row, int hkv, int head_dim, float scale,
+                       const void *out, int out_dtype, int64_t out_tok_stride) {
+  K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
+  K8V4_REQUIRE(out_dtype == K8V4_F16 || out_dtype == K8V4_BF16 || out_dtype == K8V4_F32,
+               "out dtype must be fp16, bf16 or fp32");
+  K8V4_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && v_zero && block_row && out, "null pointer");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
+               "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
+  K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
+  K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim && out_tok_stride % 4 == 0,
+               "out token stride must cover HQ*D and be a multiple of 4");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, "out must be 16-byte aligned");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && k_page_stride % 16 == 0,
+               "k_cache must keep 16-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(v_cache) % 8 == 0 && v_page_stride % 8 == 0,
+               "v_cache must keep 8-byte aligned rows");
+  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_scale) % 4 == 0 && reinterpret_cast<uintptr_t>(v_scale) % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(v_zero) % 4 == 0 && ks_page_stride % 4 == 0 &&
+                   vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
+               "scale planes must be 4-byte aligned");
+  K8V4_REQUIRE(scale > 0.f && scale < 1e30f, "softmax scale must be positive and finite");
+  return K8V4_OK;
+}
+
+// Fills the launch arguments every prefill launch shares.
+PrefillArgs prefill_base_args(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                              const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                              const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                              int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                              int64_t vz_page_stride, const int32_t *block_row, int pages_per_block, int hkv,
+                              float scale, void *out, int out_dtype, int64_t out_tok_stride) {
+  PrefillArgs a{};
+  a.q = static_cast<const uint16_t *>(q);
+  a.q_tok_stride = q_tok_stride;
+  a.q_bf16 = q_dtype == K8V4_BF16;
+  a.k_cache = k_cache;
+  a.k_scale = k_scale;
+  a.v_cache = v_cache;
+  a.v_scale = v_scale;
+  a.v_zero = v_zero;
+  a.num_pages = num_pages;
+  a.k_ps = k_page_stride;
+  a.ks_ps = ks_page_stride;
+  a.v_ps = v_page_stride;
+  a.vs_ps = vs_page_stride;
+  a.vz_ps = vz_page_stride;
+  a.block_row = block_row;
+  a.ppb = pages_per_block;
+  a.hkv = hkv;
+  a.c = scale * 1.4426950408889634f;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.out_tok_stride = out_tok_stride;
+  return a;
+}
 }  // namespace
 }  // namespace k8v4
 
@@ -1333,50 +1497,18 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   K8V4_REQUIRE(table_width >= 1 && table_width * pages_per_block * kPage >= seq_len,
                "block table row covers %lld tokens, seq_len is %lld",
                static_cast<long long>(table_width * pages_per_block * kPage), static_cast<long long>(seq_len));
-  K8V4_REQUIRE(q_dtype == K8V4_F16 || q_dtype == K8V4_BF16, "q dtype must be fp16 or bf16");
-  K8V4_REQUIRE(out_dtype == K8V4_F16 || out_dtype == K8V4_BF16 || out_dtype == K8V4_F32,
-               "out dtype must be fp16, bf16 or fp32");
-  K8V4_REQUIRE(q && k_cache && k_scale && v_cache && v_scale && v_zero && block_row && out, "null pointer");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_tok_stride % 8 == 0,
-               "q must be 16-byte aligned with a token stride that is a multiple of 8 elements");
-  K8V4_REQUIRE(q_tok_stride >= int64_t(hkv) * kGqa * head_dim, "q token stride shorter than HQ*D");
-  K8V4_REQUIRE(out_tok_stride >= int64_t(hkv) * kGqa * head_dim && out_tok_stride % 4 == 0,
-               "out token stride must cover HQ*D and be a multiple of 4");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, "out must be 16-byte aligned");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && k_page_stride % 16 == 0,
-               "k_cache must keep 16-byte aligned rows");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(v_cache) % 8 == 0 && v_page_stride % 8 == 0,
-               "v_cache must keep 8-byte aligned rows");
-  K8V4_REQUIRE(reinterpret_cast<uintptr_t>(k_scale) % 4 == 0 && reinterpret_cast<uintptr_t>(v_scale) % 4 == 0 &&
-                   reinterpret_cast<uintptr_t>(v_zero) % 4 == 0 && ks_page_stride % 4 == 0 &&
-                   vs_page_stride % 4 == 0 && vz_page_stride % 4 == 0,
-               "scale planes must be 4-byte aligned");
-  K8V4_REQUIRE(scale > 0.f && scale < 1e30f, "softmax scale must be positive and finite");
+  {
+    const int rc = check_prefill_args(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero,
+                                      k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                                      block_row, hkv, head_dim, scale, out, out_dtype, out_tok_stride);
+    if (rc) return rc;
+  }
 
-  PrefillArgs a;
-  a.q = static_cast<const uint16_t *>(q);
-  a.q_tok_stride = q_tok_stride;
-  a.q_bf16 = q_dtype == K8V4_BF16;
-  a.k_cache = k_cache;
-  a.k_scale = k_scale;
-  a.v_cache = v_cache;
-  a.v_scale = v_scale;
-  a.v_zero = v_zero;
-  a.num_pages = num_pages;
-  a.k_ps = k_page_stride;
-  a.ks_ps = ks_page_stride;
-  a.v_ps = v_page_stride;
-  a.vs_ps = vs_page_stride;
-  a.vz_ps = vz_page_stride;
-  a.block_row = block_row;
-  a.ppb = pages_per_block;
+  PrefillArgs a = prefill_base_args(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
+                                    k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                                    block_row, pages_per_block, hkv, scale, out, out_dtype, out_tok_stride);
   a.seq_len = static_cast<int>(seq_len);
   a.q_len = static_cast<int>(q_len);
-  a.hkv = hkv;
-  a.c = scale * 1.4426950408889634f;
-  a.out = out;
-  a.out_dtype = out_dtype;
-  a.out_tok_stride = out_tok_stride;
 
   PrefillPlan pl;
   K8V4_REQUIRE(plan_prefill(seq_len, q_len, hkv, head_dim, pl), "prefill too large for one call (q_len %lld, seq_len %lld)",
@@ -1431,4 +1563,115 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   else
     prefill_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS / kMergeSplit), 0, s>>>(a);
   return launch_status("k8v4_prefill_paged merge");
+}
+
+extern "C" int64_t k8v4_prefill_batch_workspace_bytes(int hkv, int head_dim) {
+  using namespace k8v4;
+  if (!supported_heads(hkv) || !supported_dim(head_dim)) return -1;
+  return partial_bytes(device_cus(), head_dim);
+}
+
+extern "C" int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
+                                        const float *k_scale, const uint8_t *v_cache, const float *v_scale,
+                                        const float *v_zero, int64_t num_pages, int64_t k_page_stride,
+                                        int64_t ks_page_stride, int64_t v_page_stride, int64_t vs_page_stride,
+                                        int64_t vz_page_stride, const int32_t *block_table, int64_t bt_stride,
+                                        int64_t table_width, int pages_per_block, int nseq, const int64_t *tok0,
+                                        const int64_t *q_lens, const int64_t *seq_lens, const int64_t *rows,
+                                        int hkv, int head_dim, float scale, void *out, int out_dtype,
+                                        int64_t out_tok_stride, void *workspace, int64_t workspace_bytes,
+                                        void *stream) {
+  using namespace k8v4;
+  clear_error();
+  K8V4_REQUIRE(supported_heads(hkv), "unsupported per-GPU KV head count %d (this library serves 2 or 4)", hkv);
+  K8V4_REQUIRE(supported_dim(head_dim), "unsupported head dim %d (this library serves 128 or 256)", head_dim);
+  K8V4_REQUIRE(nseq >= 0, "negative sequence count");
+  if (nseq == 0) return K8V4_OK;
+  K8V4_REQUIRE(tok0 && q_lens && seq_lens && rows, "null pointer");
+  K8V4_REQUIRE(pages_per_block >= 1, "pages_per_block");
+  K8V4_REQUIRE(num_pages >= 1, "empty cache");
+  K8V4_REQUIRE(table_width >= 1 && bt_stride >= table_width, "block table row stride shorter than its width");
+  {
+    const int rc = check_prefill_args(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero,
+                                      k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                                      block_table, hkv, head_dim, scale, out, out_dtype, out_tok_stride);
+    if (rc) return rc;
+  }
+  for (int i = 0; i < nseq; ++i) {
+    K8V4_REQUIRE(q_lens[i] >= 0 && seq_lens[i] >= 0 && seq_lens[i] < (int64_t(1) << 30),
+                 "sequence %d: bad lengths", i);
+    K8V4_REQUIRE(q_lens[i] <= seq_lens[i], "sequence %d: query longer than the KV sequence", i);
+    K8V4_REQUIRE(tok0[i] >= 0 && rows[i] >= 0, "sequence %d: negative token offset or table row", i);
+    K8V4_REQUIRE(table_width * pages_per_block * kPage >= seq_lens[i],
+                 "sequence %d: block table row covers %lld tokens, seq_len is %lld", i,
+                 static_cast<long long>(table_width * pages_per_block * kPage), static_cast<long long>(seq_lens[i]));
+  }
+  const int64_t need = partial_bytes(device_cus(), head_dim);
+  K8V4_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "prefill workspace must be a 16-byte aligned device buffer");
+  if (workspace_bytes < need) {
+    set_error("prefill workspace holds %lld bytes, the call needs %lld", static_cast<long long>(workspace_bytes),
+              static_cast<long long>(need));
+    return K8V4_ERR_WORKSPACE;
+  }
+  PrefillArgs a = prefill_base_args(q, q_dtype, q_tok_stride, k_cache, k_scale, v_cache, v_scale, v_zero, num_pages,
+                                    k_page_stride, ks_page_stride, v_page_stride, vs_page_stride, vz_page_stride,
+                                    block_table, pages_per_block, hkv, scale, out, out_dtype, out_tok_stride);
+  a.rows = rows_per_block(head_dim);
+  a.ws = static_cast<float *>(workspace);
+  a.head0 = 0;
+  a.tiles = nullptr;
+  auto s = static_cast<hipStream_t>(stream);
+  // Launches of up to kBatchMax non-empty sequences each, one after another
+  // on the stream (each launch reuses the workspace after the previous one).
+  const int ob = out_dtype == K8V4_F32 ? 4 : 2;
+  int i = 0;
+  while (i < nseq) {
+    PrefillBatchArgs ba{};
+    int64_t steps = 0, blocks = 0;
+    for (; i < nseq && ba.n < kBatchMax; ++i) {
+      if (q_lens[i] == 0) continue;
+      PrefillPlan pl;
+      K8V4_REQUIRE(plan_prefill(seq_lens[i], q_lens[i], hkv, head_dim, pl),
+                   "sequence %d too large for one call (q_len %lld, seq_len %lld)", i,
+                   static_cast<long long>(q_lens[i]), static_cast<long long>(seq_lens[i]));
+      const int k = ba.n++;
+      PrefillArgs &sa = ba.seq[k];
+      sa = a;
+      sa.q = a.q + tok0[i] * q_tok_stride;
+      sa.out = static_cast<char *>(out) + tok0[i] * out_tok_stride * ob;
+      sa.block_row = block_table + rows[i] * bt_stride;
+      sa.q_len = static_cast<int>(q_lens[i]);
+      sa.seq_len = static_cast<int>(seq_lens[i]);
+      sa.nbh = pl.nbh;
+      sa.tper = pl.tper;
+      ba.step0[k] = static_cast<int>(steps);
+      ba.block0[k] = static_cast<int>(blocks);
+      steps += pl.total;
+      blocks += static_cast<int64_t>(pl.nbh) * hkv;
+      K8V4_REQUIRE(steps < (int64_t(1) << 30) && blocks * kMergeSplit < (int64_t(1) << 30),
+                   "prefill batch too large for one launch");
+    }
+    if (ba.n == 0) break;
+    ba.step0[ba.n] = static_cast<int>(steps);
+    ba.block0[ba.n] = static_cast<int>(blocks);
+    int64_t grid = std::min<int64_t>(static_cast<int64_t>(device_cus()), steps);
+    if (grid >= 8) grid -= grid % 8;
+    for (int k = 0; k < ba.n; ++k) {
+      ba.seq[k].total = static_cast<int>(steps);
+      ba.seq[k].grid = static_cast<int>(grid);
+      ba.seq[k].xcd_perm = grid % 8 == 0 ? 1 : 0;
+    }
+    const dim3 mgrid(static_cast<unsigned>(blocks * kMergeSplit));
+    if (head_dim == 128) {
+      prefill_batch_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<128>::THREADS), 0, s>>>(ba);
+      prefill_batch_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(ba);
+    } else {
+      prefill_batch_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<256>::THREADS), 0, s>>>(ba);
+      prefill_batch_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS / kMergeSplit), 0, s>>>(ba);
+    }
+    const int rc = launch_status("k8v4_prefill_paged_batch");
+    if (rc) return rc;
+  }
+  return K8V4_OK;
 }

@@ -41,7 +41,7 @@ from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_b
 from vllm.v1.kv_cache_interface import AttentionSpec
 
 from .cache_views import bind_regions
-from .layout import CACHE_DTYPE, DECODE_MAX_T, PAGE, PageLayout, attention_pages_per_block
+from .layout import CACHE_DTYPE, DECODE_MAX_T, GQA, PAGE, PageLayout, attention_pages_per_block
 from .ops_api import ops
 from .plan import layout_for_heads, query_segments, require_decoder, scratch_capacity, token_span, uniform_packed_q_len
 from .scratch import Scratch, ensure_scratch, get_scratch, scratch_ready
@@ -287,8 +287,12 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
             self._decode(q, out, regions, meta, run, scratch)
         if meta.prefill_seqs:
             lens = meta.seq_lens_cpu if meta.seq_lens_cpu is not None else meta.seq_lens.detach().cpu()
+            short = [seq for seq in meta.prefill_seqs if _batched_prefill(seq.width, lay.head_dim)]
+            if short:
+                self._prefill_batch(q, out, regions, meta, short, lens, scratch)
             for seq in meta.prefill_seqs:
-                self._prefill(q, out, regions, meta, seq, int(lens[seq.req]), scratch)
+                if not _batched_prefill(seq.width, lay.head_dim):
+                    self._prefill(q, out, regions, meta, seq, int(lens[seq.req]), scratch)
         return output
 
     def _decode(self, q, out, regions, meta: Xe2K8V4Metadata, run: DecodeRun, scratch: Scratch) -> None:
@@ -311,11 +315,23 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
         ops().int8k_int4v_attn_batch(q[rows], None, None, *regions, table, lens, None, scratch.decode_ws,
                                      None, None, None, out[rows], run.q_len, meta.pages_per_block)
 
+    def _prefill_batch(self, q, out, regions, meta: Xe2K8V4Metadata, seqs: list[PrefillSeq], lens,
+                       scratch: Scratch) -> None:
+        """The step's short chunks in one call (the reference runs one prefill per
+        request, backend.py:376-409)."""
+        seq_lens = [int(lens[seq.req]) for seq in seqs]
+        for seq, seq_len in zip(seqs, seq_lens):
+            _check_covers(seq_len, seq.width)
+        table = meta.block_table
+        if table.dtype != torch.int32 or table.dim() != 2 or table.stride(1) != 1:
+            table = table.to(torch.int32).contiguous()
+        ops().prefill_paged_batch(q, *regions, table, [seq.tok0 for seq in seqs], [seq.width for seq in seqs],
+                                  seq_lens, [seq.req for seq in seqs], meta.pages_per_block, self.scale, out,
+                                  workspace=scratch.prefill_ws)
+
     def _prefill(self, q, out, regions, meta: Xe2K8V4Metadata, seq: PrefillSeq, seq_len: int,
                  scratch: Scratch) -> None:
-        if seq_len < seq.width:
-            raise RuntimeError("seq_len %d does not cover query %d; the kernel expects the length to include "
-                               "this step" % (seq_len, seq.width))
+        _check_covers(seq_len, seq.width)
         row = meta.block_table[seq.req]
         if row.dtype != torch.int32 or not row.is_contiguous():
             row = row.to(torch.int32).contiguous()
@@ -325,6 +341,23 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
 
 
 # ----------------------------------------------------------------- helpers
+# Chunks the single prefill entry would run with its in-kernel page conversion
+# (at head dim 128, up to three row blocks of 256 query rows: 128 tokens; at
+# head dim 256 always) gain nothing from running alone: a step's share one
+# batched launch.  Longer chunks at head dim 128 keep the entry that
+# dequantizes each page once per KV head.
+_BATCHED_PREFILL_TOKENS_D128 = 3 * 256 // GQA
+
+
+def _batched_prefill(width: int, head_dim: int) -> bool:
+    return head_dim == 256 or width <= _BATCHED_PREFILL_TOKENS_D128
+
+
+def _check_covers(seq_len: int, width: int) -> None:
+    if seq_len < width:
+        raise RuntimeError("seq_len %d does not cover query %d; the kernel expects the length to include "
+                           "this step" % (seq_len, width))
+
 def _cache_tensor(kv_cache) -> torch.Tensor:
     """The layer's one packed cache tensor (vLLM may hand it over in a list)."""
     if isinstance(kv_cache, (list, tuple)):

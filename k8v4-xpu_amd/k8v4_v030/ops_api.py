@@ -74,6 +74,13 @@ _EXTRA_SYMBOLS.append((
     _i32,
 ))
 _EXTRA_SYMBOLS.append(("k8v4_prefill_workspace_bytes", [_i64, _i64, _i32, _i32], _i64))
+_EXTRA_SYMBOLS.append((
+    "k8v4_prefill_paged_batch",
+    [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+     _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, ctypes.c_float, _vp, _i32, _i64, _vp, _i64, _vp],
+    _i32,
+))
+_EXTRA_SYMBOLS.append(("k8v4_prefill_batch_workspace_bytes", [_i32, _i32], _i64))
 _EXTRA_SYMBOLS.append(("k8v4_k_store_paged", [_vp, _i32, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _i64, _vp],
                        _i32))
 _EXTRA_SYMBOLS.append(("k8v4_v_store_paged",
@@ -410,6 +417,68 @@ class _Ops:
             _ptr(workspace), int(workspace.numel()) * workspace.element_size(),
         ]
         return BoundCall(self._lib, self._lib.k8v4_prefill_paged, args, dev, tensors)
+
+    def prefill_batch_workspace_bytes(self, hkv: int, head_dim: int) -> int:
+        """Scratch bytes :meth:`prefill_paged_batch` needs (any sequences)."""
+        n = int(self._lib.k8v4_prefill_batch_workspace_bytes(int(hkv), int(head_dim)))
+        _require(n >= 0, "bad shape for the prefill workspace")
+        return n
+
+    def prefill_paged_batch(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, tok0, q_lens,
+                            seq_lens, rows, pages_per_block: int, scale: float, out, workspace=None):
+        """Several sequences' prefill in one call (the chunks of one step).
+
+        Sequence i: query rows ``q[tok0[i] : tok0[i] + q_lens[i]]`` (bottom-right
+        causal over its ``seq_lens[i]`` keys) into the same rows of ``out``, its
+        pages in ``block_table[rows[i]]``.  ``tok0``, ``q_lens``, ``seq_lens`` and
+        ``rows`` are Python integer sequences of one length.  Same numerics as
+        :meth:`prefill_paged` per sequence."""
+        _require(q.dim() == 3, "query [T,HQ,D]")
+        head_dim = int(q.shape[2])
+        _require(head_dim in (128, 256), "query [T,HQ,D] with D in (128, 256)")
+        hkv = int(k_cache.shape[2]) if k_cache.dim() == 4 else -1
+        _require(int(q.shape[1]) == GQA * hkv,
+                 "query has %d heads, the K8/V4 cache holds %d (needs %d)" % (int(q.shape[1]), hkv, GQA * hkv))
+        _checked_hkv(hkv)
+        check_paged_k(k_cache, k_scale, hkv, head_dim)
+        check_paged_v(v_cache, v_scale, v_zero, hkv, head_dim)
+        tok0, q_lens, seq_lens, rows = ([int(x) for x in v] for v in (tok0, q_lens, seq_lens, rows))
+        n = len(tok0)
+        _require(len(q_lens) == n and len(seq_lens) == n and len(rows) == n,
+                 "tok0, q_lens, seq_lens and rows must have one length")
+        _require(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1,
+                 "block_table must be int32 [B, W] with unit column stride")
+        tokens = int(q.shape[0])
+        for t0, ql, sl, r in zip(tok0, q_lens, seq_lens, rows):
+            if ql > sl:
+                raise RuntimeError("query longer than the KV sequence")
+            _require(ql >= 0 and t0 >= 0 and t0 + ql <= tokens, "sequence rows outside the query")
+            _require(0 <= r < int(block_table.shape[0]), "block table row out of range")
+        if n == 0 or max(q_lens) == 0:
+            return
+        _require(q.dtype in (torch.float16, torch.bfloat16), "query must be float16 or bfloat16")
+        _require(q.stride(2) == 1 and q.stride(1) == head_dim, "query head/dim strides")
+        _require(out.shape == q.shape, "out shape")
+        _require(out.dtype in (torch.float16, torch.bfloat16, torch.float32), "out float16, bfloat16 or float32")
+        _require(out.stride(2) == 1 and out.stride(1) == head_dim, "out head/dim strides")
+        _require(int(pages_per_block) >= 1, "pages_per_block")
+        tensors = (q, k_cache, k_scale, v_cache, v_scale, v_zero, block_table, out)
+        dev = _on_gpu(*tensors)
+        need = self.prefill_batch_workspace_bytes(hkv, head_dim)
+        if workspace is None:
+            workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=dev)
+        _require(workspace.is_contiguous() and workspace.device == dev, "prefill workspace must be a contiguous "
+                 "buffer on the query's device")
+        arrays = [(ctypes.c_int64 * n)(*v) for v in (tok0, q_lens, seq_lens, rows)]
+        row_stride = GQA * hkv * head_dim
+        rc = self._lib.k8v4_prefill_paged_batch(
+            _ptr(q), _DTYPE_CODE[q.dtype], int(q.stride(0)) if tokens > 1 else row_stride,
+            *cache_args(k_cache, k_scale, v_cache, v_scale, v_zero),
+            _ptr(block_table), int(block_table.stride(0)), int(block_table.shape[1]), int(pages_per_block), n,
+            *[ctypes.cast(x, ctypes.c_void_p) for x in arrays], hkv, head_dim, float(scale),
+            _ptr(out), _DTYPE_CODE[out.dtype], int(out.stride(0)) if tokens > 1 else row_stride,
+            _ptr(workspace), int(workspace.numel()) * workspace.element_size(), _stream(dev))
+        _check(rc, self._lib)
 
     # -- K-only / V-only stores ----------------------------------------------
     def k_store_paged(self, k_fp16, slot_mapping, k_cache, k_scale):

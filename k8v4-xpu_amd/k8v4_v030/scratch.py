@@ -10,7 +10,8 @@ a captured HIP graph keeps stable addresses and no call allocates:
 * the prefill workspace -- partial softmax states of the row blocks that
   ``k8v4_prefill_paged`` splits between work-groups, sized by the library
   (``k8v4_prefill_workspace_bytes``) for the longest chunk over the longest
-  context.
+  context, and at least what one launch of ``k8v4_prefill_paged_batch``
+  (a step's short chunks together) needs.
 
 Capacity is given in the reference's terms (k8v4_v030/scratch.py:17-115):
 ``nprog_max`` = kernel pages of the longest sequence times the KV head count,
@@ -54,10 +55,13 @@ def decode_workspace_bytes(layout: PageLayout, max_pages: int, max_out_tokens: i
 
 
 def prefill_workspace_bytes(layout: PageLayout, max_pages: int, max_chunk: int) -> int:
-    """Prefill workspace for a ``max_chunk``-token query over ``max_pages`` pages of context."""
+    """Prefill workspace for a ``max_chunk``-token query over ``max_pages`` pages of
+    context, and for a batch of a step's short chunks in one call."""
     seq_len = int(max_pages) * PAGE
     chunk = max(1, min(int(max_chunk), seq_len))
-    return _library_ops().prefill_workspace_bytes(seq_len, chunk, layout.hkv, layout.head_dim)
+    lib = _library_ops()
+    return max(lib.prefill_workspace_bytes(seq_len, chunk, layout.hkv, layout.head_dim),
+               lib.prefill_batch_workspace_bytes(layout.hkv, layout.head_dim))
 
 
 class Scratch:

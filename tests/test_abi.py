@@ -171,3 +171,49 @@ def test_every_reference_op_name_is_in_the_table(lib):
              "int8k_int4v_s1_varlen_from_q", "int8k_int4v_decode_step", "int8k_int4v_attn_batch"]
     o = ops_api.ops()
     assert all(callable(getattr(o, n)) for n in names)
+
+
+def _prefill_batch(lib, tok0, q_lens, seq_lens, rows, **over):
+    """k8v4_prefill_paged_batch with plausible host arguments and fake (never dereferenced) pointers."""
+    import ctypes
+
+    p = 0x10000
+    n = len(tok0)
+    arrs = [(ctypes.c_int64 * max(n, 1))(*v) for v in (tok0, q_lens, seq_lens, rows)]
+    a = dict(q=p, q_dtype=0, q_tok_stride=24 * 128, k_cache=p, k_scale=p, v_cache=p, v_scale=p, v_zero=p,
+             num_pages=64, ks=52224, kss=52224, vs=52224, vss=52224, vzs=52224, bt=p, bt_stride=32, width=32,
+             ppb=1, nseq=n, tok0=ctypes.cast(arrs[0], ctypes.c_void_p), q_lens=ctypes.cast(arrs[1], ctypes.c_void_p),
+             seq_lens=ctypes.cast(arrs[2], ctypes.c_void_p), rows=ctypes.cast(arrs[3], ctypes.c_void_p), hkv=4,
+             d=128, scale=0.088, out=p, out_dtype=0, out_stride=24 * 128, ws=p, ws_bytes=0, stream=None)
+    a.update(over)
+    return lib.k8v4_prefill_paged_batch(*a.values())
+
+
+def test_prefill_batch_host_checks(lib):
+    """The batched prefill checks each sequence like the single entry, before any launch."""
+    assert _prefill_batch(lib, [], [], [], []) == 0  # nothing to do
+    assert _prefill_batch(lib, [0], [5], [100], [0], hkv=3) == 1
+    assert "unsupported per-GPU KV head count 3" in lib.k8v4_last_error().decode()
+    assert _prefill_batch(lib, [0, 9], [5, 9], [100, 8], [0, 1]) == 1
+    assert "sequence 1: query longer than the KV sequence" in lib.k8v4_last_error().decode()
+    assert _prefill_batch(lib, [0], [5], [64 * 32 + 1], [0]) == 1
+    assert "block table row covers 2048 tokens" in lib.k8v4_last_error().decode()
+    assert _prefill_batch(lib, [0], [5], [100], [-1]) == 1
+    assert "negative" in lib.k8v4_last_error().decode()
+    assert _prefill_batch(lib, [0], [5], [100], [0], bt_stride=16) == 1
+    assert "stride" in lib.k8v4_last_error().decode()
+    assert _prefill_batch(lib, [0], [5], [100], [0], q=0x10008) == 1
+    assert "16-byte" in lib.k8v4_last_error().decode()
+    # A workspace smaller than one launch's partial states: K8V4_ERR_WORKSPACE, nothing launched.
+    assert _prefill_batch(lib, [0], [5], [100], [0], ws_bytes=1024) == 2
+    assert "prefill workspace holds 1024 bytes" in lib.k8v4_last_error().decode()
+
+
+def test_prefill_batch_workspace_covers_every_short_single_call(lib):
+    for hkv, d in ((4, 128), (2, 128), (2, 256), (4, 256)):
+        need = lib.k8v4_prefill_batch_workspace_bytes(hkv, d)
+        assert need > 0
+        for q_len, seq_len in ((1, 64), (40, 2000), (128, 9000)):  # up to three row blocks: no tile pre-pass
+            assert lib.k8v4_prefill_workspace_bytes(seq_len, q_len, hkv, d) <= need
+    assert lib.k8v4_prefill_batch_workspace_bytes(3, 128) == -1
+    assert lib.k8v4_prefill_batch_workspace_bytes(4, 64) == -1

@@ -135,6 +135,40 @@ def test_mixed_step_runs_decode_batched_and_prefill_per_request():
         t0 += rows
 
 
+def test_mixed_step_batches_the_short_prefills():
+    """Decode rows, four short chunks (12 to 128 tokens: one batched prefill
+    launch) and a 129-token chunk (the single entry) in one step."""
+    lay = PageLayout(4, 128)
+    impl = make_impl()
+    builder = make_builder(device=DEV)
+    gen = torch.Generator().manual_seed(21)
+    q_lens = [1, 1, 30, 64, 128, 129, 12]
+    lengths = [500, 64, 400, 64, 900, 1300, 77]
+    table = _table(gen, lengths, 120, 64, 24)
+    cache = vllm_cache(120, 64, lay, DEV)
+    _fill(impl, cache, gen, table, [L - q for L, q in zip(lengths, q_lens)], 64, lay, torch.float16)
+    ntok = sum(q_lens)
+    q, k, v = _qkv(gen, ntok, lay, torch.float16)
+    slots = torch.cat([slots_for(table[b], range(L - ql, L), 64) for b, (L, ql) in enumerate(zip(lengths, q_lens))])
+    meta = builder.build(0, common_metadata(q_lens, lengths, table, slots, DEV))
+    assert [s.width for s in meta.prefill_seqs] == [30, 64, 128, 129, 12]
+    impl.do_kv_cache_update(None, k, v, cache, meta.slot_mapping)
+    out = torch.full((ntok, 24, 128), float("nan"), dtype=torch.float16, device=DEV)
+    impl.forward(None, q, k, v, cache, meta, out)
+    blob, geom = _blob(cache), paged.Geometry(4, 128)
+    got = out.float().cpu().numpy()
+    qf = q.float().cpu().numpy()
+    want_dec = attention.decode_attention(qf[:2], blob, geom, table[:2].numpy(), np.array(lengths[:2]), 1)
+    assert_close(got[:2], want_dec, what="decode rows")
+    t0 = 2
+    for b in range(2, len(q_lens)):
+        rows = q_lens[b]
+        want = attention.prefill_attention(qf[t0 : t0 + rows], blob, geom, table[b].numpy(), lengths[b], 1,
+                                           1.0 / math.sqrt(128))
+        assert_close(got[t0 : t0 + rows], want, what="prefill rows of request %d" % b)
+        t0 += rows
+
+
 def test_manager_blocks_of_33_pages_at_d256():
     """The reference's deployment shape: TP2 rank (2 KV / 12 Q heads), D = 256,
     2,112-token manager blocks addressed directly (33 kernel pages per entry)."""
@@ -191,7 +225,7 @@ def test_step_allocates_nothing_after_the_scratch():
     impl = make_impl()
     builder = make_builder(device=DEV)
     gen = torch.Generator().manual_seed(16)
-    q_lens, lengths = [7, 7, 300], [900, 700, 1500]
+    q_lens, lengths = [7, 7, 300, 40], [900, 700, 1500, 600]
     table = _table(gen, lengths, 60, 64, 24)
     cache = vllm_cache(60, 64, lay, DEV)
     _fill(impl, cache, gen, table, [L - q for L, q in zip(lengths, q_lens)], 64, lay, torch.float16)
