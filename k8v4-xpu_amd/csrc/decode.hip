@@ -123,24 +123,32 @@ __device__ __forceinline__ int seq_pages(const DecodeArgs &a, int b) {
   return static_cast<int>(n < cap ? n : cap);
 }
 
-__device__ __forceinline__ int wave_sum(int x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, kWave);
+// Wave-wide scans of non-negative ints by DPP moves (register to register,
+// a few cycles each; the LDS permutes a shuffle compiles to cost a round trip
+// through the LDS unit per step, and the plan is on the critical path of
+// every work-group's prologue).  Within each 16-lane row, row_shr 1, 2, 4, 8
+// (a lane with no source in its row reads 0); then lane 15 of rows 0 and 2 is
+// added to rows 1 and 3 (row_bcast:15) and lane 31 to rows 2 and 3
+// (row_bcast:31).  All 64 lanes must be active.
+template <bool MAX>
+__device__ __forceinline__ int dpp_step(int x, int y) {
+  return MAX ? max(x, y) : x + y;
+}
+template <bool MAX>
+__device__ __forceinline__ int wave_scan_dpp(int x) {
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false));  // row_shr:1
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false));  // row_shr:2
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false));  // row_shr:4
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false));  // row_shr:8
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));  // row_bcast:31
   return x;
 }
-__device__ __forceinline__ int wave_max(int x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x = max(x, __shfl_xor(x, m, kWave));
-  return x;
-}
-__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int y = __shfl_up(x, d, kWave);
-    if (lane >= d) x += y;
-  }
-  return x;
-}
+// Sum / max over the wave (x >= 0), the same value in every lane.
+__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_scan_dpp<false>(x), kWave - 1); }
+__device__ __forceinline__ int wave_max(int x) { return __builtin_amdgcn_readlane(wave_scan_dpp<true>(x), kWave - 1); }
+// Inclusive prefix sum over the lanes (x >= 0).
+__device__ __forceinline__ int wave_inclusive_scan(int x) { return wave_scan_dpp<false>(x); }
 
 // Pages per split for this batch (same value in every lane and work-group).
 __device__ int plan_pages_per_split(const DecodeArgs &a, int lane) {
@@ -173,7 +181,7 @@ __device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want
     const int b = b0 + lane;
     const int n = b < a.batch ? seq_pages(a, b) : 0;
     const int s = (n + P - 1) / P;
-    const int incl = wave_inclusive_scan(s, lane);
+    const int incl = wave_inclusive_scan(s);
     const int excl = base + incl - s;
     bool hit;
     if (want_b >= 0)
@@ -185,11 +193,11 @@ __device__ SplitRange plan_locate(const DecodeArgs &a, int P, int lane, int want
       const int src = __builtin_ctzll(mask);
       // The results are wave-uniform; readfirstlane keeps them in SGPRs.
       r.b = __builtin_amdgcn_readfirstlane(b0 + src);
-      r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, src, kWave));
-      r.count = __builtin_amdgcn_readfirstlane(__shfl(s, src, kWave));
+      r.first = __builtin_amdgcn_readlane(excl, src);
+      r.count = __builtin_amdgcn_readlane(s, src);
       return r;
     }
-    base += __shfl(incl, kWave - 1, kWave);
+    base += __builtin_amdgcn_readlane(incl, kWave - 1);
   }
   return r;
 }
@@ -224,7 +232,7 @@ __device__ SplitPlan plan_split(const DecodeArgs &a, int lane, int wg) {
   int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
   P = __builtin_amdgcn_readfirstlane(max(max(P, a.min_pages), 1));
   const int s = (n + P - 1) / P;
-  const int excl = wave_inclusive_scan(s, lane) - s;
+  const int excl = wave_inclusive_scan(s) - s;
   const uint64_t mask = __ballot(s > 0 && wg >= excl && wg < excl + s);
   sp.P = P;
   sp.r = SplitRange{-1, 0, 0};
@@ -233,10 +241,10 @@ __device__ SplitPlan plan_split(const DecodeArgs &a, int lane, int wg) {
   if (mask) {
     const int src = __builtin_ctzll(mask);
     sp.r.b = __builtin_amdgcn_readfirstlane(src);
-    sp.r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, src, kWave));
-    sp.r.count = __builtin_amdgcn_readfirstlane(__shfl(s, src, kWave));
-    sp.npages = __builtin_amdgcn_readfirstlane(__shfl(n, src, kWave));
-    sp.L0 = __builtin_amdgcn_readfirstlane(__shfl(L, src, kWave));
+    sp.r.first = __builtin_amdgcn_readlane(excl, src);
+    sp.r.count = __builtin_amdgcn_readlane(s, src);
+    sp.npages = __builtin_amdgcn_readlane(n, src);
+    sp.L0 = __builtin_amdgcn_readlane(L, src);
   }
   return sp;
 }
@@ -251,11 +259,11 @@ __device__ SplitRange plan_sequence(const DecodeArgs &a, int lane, int want_b) {
   int P = a.grid > a.batch ? (total + (a.grid - a.batch) - 1) / (a.grid - a.batch) : maxn;
   P = __builtin_amdgcn_readfirstlane(max(max(P, a.min_pages), 1));
   const int s = (n + P - 1) / P;
-  const int excl = wave_inclusive_scan(s, lane) - s;
+  const int excl = wave_inclusive_scan(s) - s;
   SplitRange r;
   r.b = want_b;
-  r.first = __builtin_amdgcn_readfirstlane(__shfl(excl, want_b, kWave));
-  r.count = __builtin_amdgcn_readfirstlane(__shfl(s, want_b, kWave));
+  r.first = __builtin_amdgcn_readlane(excl, want_b);
+  r.count = __builtin_amdgcn_readlane(s, want_b);
   return r;
 }
 
@@ -1220,61 +1228,14 @@ void decode_split_kernel(DecodeArgs a) {
   // Only the first chunk's K and V groups go out before the quantization
   // (register query words wait for every vector load issued before their
   // first use); the rest of the ring is filled right after it.
-  // Physical pages of this split's run, looked up once: lane l of ptab[i]
-  // holds page p0 + 64 i + l (-1 outside the cache), read back per chunk
-  // with v_readlane (no scalar-cache miss or page division in the loop).
-  // Runs longer than 128 pages look their pages up as they go.
-  const bool tab_vgpr = p1 - p0 <= 128;
-  int ptab[2] = {-1, -1};
-  if (tab_vgpr) {
-    // Both entries are loaded before either is used (one round trip; a lane
-    // past the run reads the run's last entry and is dropped below).
-    int raw[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = min(p0 + 64 * i + lane, p1 - 1);
-      raw[i] = bt_row[a.ppb <= 1 ? p : p / a.ppb];
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int p = p0 + 64 * i + lane;
-      const int ph = a.ppb <= 1 ? raw[i] : raw[i] * a.ppb + p % a.ppb;
-      ptab[i] = (p < p1 && ph >= 0 && ph < a.num_pages) ? ph : -1;
-    }
-  }
-  auto page_of = [&](int x) -> int {  // x: chunk index in the sequence (wave-uniform)
-    const int p = x >> 1;
-    if (tab_vgpr) {
-      const int d = p - p0;
-      const int lo_pg = __builtin_amdgcn_readlane(ptab[0], d & 63);
-      const int hi_pg = __builtin_amdgcn_readlane(ptab[1], d & 63);
-      return d < 64 ? lo_pg : hi_pg;
-    }
-    const int ph = physical_page(a, bt_row, p);
-    return (ph >= 0 && ph < a.num_pages) ? ph : -1;
-  };
   int issued = 0;
-  int mk[4] = {0, 0, 0, 0}, mv[4] = {0, 0, 0, 0};
-  uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
-  auto fill_slot = [&](int s) {
-    if (s >= cnt) return;
-    const int xs = my0 + s * NWH;
-    if (s < RK) {
-      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xs), xs, lo, kring + s * S::K_BYTES)) << s;
-      issued += S::NK;
-      mk[s] = issued;
-    }
-    if (s < RV) {
-      issue_v<D, HKV, PH>(a, page_of(xs), xs, lo, lane, vring + s * S::V_BYTES);
-      issued += S::NVS;
-      mv[s] = issued;
-    }
-  };
   // Q in LDS: this wave's query rows (its tiles nt = w, w + NWH, ...) go by
   // direct-to-LDS loads into its K slots 1.. (filled only after the
-  // quantization), ahead of the first chunk's loads; waiting for them is then
-  // a plain count of this wave's own loads.  Rows past the last query row
-  // load row 0 and are zeroed below.
+  // quantization), ahead of the block-table loads below, so the two round
+  // trips overlap (the first chunk's loads need the table entries; the
+  // quantization needs only these rows).  Waiting for them is then a plain
+  // count of this wave's own loads.  Rows past the last query row load row 0
+  // and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
   if (QSPLIT && !PH && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
@@ -1319,6 +1280,55 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
   const int q_done = issued;
+  // Physical pages of this split's run, looked up once: lane l of ptab[i]
+  // holds page p0 + 64 i + l (-1 outside the cache), read back per chunk
+  // with v_readlane (no scalar-cache miss or page division in the loop).
+  // Runs longer than 128 pages look their pages up as they go.
+  const bool tab_vgpr = p1 - p0 <= 128;
+  int ptab[2] = {-1, -1};
+  if (tab_vgpr) {
+    // Both entries are loaded before either is used (one round trip; a lane
+    // past the run reads the run's last entry and is dropped below).
+    int raw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = min(p0 + 64 * i + lane, p1 - 1);
+      raw[i] = bt_row[a.ppb <= 1 ? p : p / a.ppb];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = p0 + 64 * i + lane;
+      const int ph = a.ppb <= 1 ? raw[i] : raw[i] * a.ppb + p % a.ppb;
+      ptab[i] = (p < p1 && ph >= 0 && ph < a.num_pages) ? ph : -1;
+    }
+  }
+  auto page_of = [&](int x) -> int {  // x: chunk index in the sequence (wave-uniform)
+    const int p = x >> 1;
+    if (tab_vgpr) {
+      const int d = p - p0;
+      const int lo_pg = __builtin_amdgcn_readlane(ptab[0], d & 63);
+      const int hi_pg = __builtin_amdgcn_readlane(ptab[1], d & 63);
+      return d < 64 ? lo_pg : hi_pg;
+    }
+    const int ph = physical_page(a, bt_row, p);
+    return (ph >= 0 && ph < a.num_pages) ? ph : -1;
+  };
+  int mk[4] = {0, 0, 0, 0}, mv[4] = {0, 0, 0, 0};
+  uint32_t valid_mask = 0;  // bit s: K slot s holds a chunk of a valid page
+  auto fill_slot = [&](int s) {
+    if (s >= cnt) return;
+    const int xs = my0 + s * NWH;
+    if (s < RK) {
+      valid_mask |= static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xs), xs, lo, kring + s * S::K_BYTES)) << s;
+      issued += S::NK;
+      mk[s] = issued;
+    }
+    if (s < RV) {
+      issue_v<D, HKV, PH>(a, page_of(xs), xs, lo, lane, vring + s * S::V_BYTES);
+      issued += S::NVS;
+      mv[s] = issued;
+    }
+  };
   fill_slot(0);
   if constexpr (PH) {
 #pragma unroll
