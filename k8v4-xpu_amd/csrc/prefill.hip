@@ -1370,9 +1370,26 @@ struct PrefillPlan {
 // of 1; 8 gave no more).
 constexpr int64_t kMinSteps = 4;
 
-// Host mirror of the device schedule; false if the call is too large for it.
 int rows_per_block(int head_dim) { return head_dim == 128 ? Tile<128>::ROWS : Tile<256>::ROWS; }
 
+// Head dim 128 dequantizes each page once per KV head into the workspace when
+// that work is shared by at least this many row blocks (below it the
+// in-kernel conversion costs less than the extra tile traffic).
+constexpr int kPreMinBlocks = 4;
+
+bool use_tiles(const PrefillPlan &pl, int head_dim) { return head_dim == 128 && pl.nbh >= kPreMinBlocks; }
+
+// Persistent work-groups for a launch of `steps` page steps: one per CU, each
+// with at least kMinSteps steps (a work-group's fixed work -- its query rows,
+// its partial state, the merge's reads of it -- outweighs a page or two of
+// attention), a multiple of 8 from 8 up (whole XCDs).
+int64_t persistent_grid(int64_t steps) {
+  int64_t grid = std::min<int64_t>(static_cast<int64_t>(device_cus()), std::max<int64_t>(1, steps / kMinSteps));
+  if (grid >= 8) grid -= grid % 8;
+  return grid;
+}
+
+// Host mirror of the device schedule; false if the call is too large for it.
 bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, int head_dim, PrefillPlan &pl) {
   const int64_t R = rows_per_block(head_dim);
   const int64_t nbh = (q_len * kGqa + R - 1) / R;
@@ -1383,28 +1400,18 @@ bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, int head_dim, Prefill
   }
   const int64_t total = tper * hkv;
   if (nbh < 1 || total < 1 || total >= (int64_t(1) << 31) / 2) return false;
-  // One work-group per CU, each with at least kMinSteps page steps: a
-  // work-group's fixed work (its query rows, its partial state, the merge's
-  // reads of it) outweighs a page or two of attention.
-  int64_t grid = std::min<int64_t>(static_cast<int64_t>(device_cus()), std::max<int64_t>(1, total / kMinSteps));
-  if (grid >= 8) grid -= grid % 8;
   pl.nbh = static_cast<int>(nbh);
   pl.tper = static_cast<int>(tper);
   pl.total = static_cast<int>(total);
-  pl.grid = static_cast<int>(grid);
+  // The grid of the launch that runs: one per KV head over its tper steps
+  // with tile images, else one over all heads.
+  pl.grid = static_cast<int>(persistent_grid(use_tiles(pl, head_dim) ? tper : total));
   return true;
 }
 
 int64_t partial_bytes(int grid, int head_dim) {
   return static_cast<int64_t>(grid) * 2 * rows_per_block(head_dim) * (head_dim + 2) * 4;
 }
-
-// Head dim 128 dequantizes each page once per KV head into the workspace when
-// that work is shared by at least this many row blocks (below it the
-// in-kernel conversion costs less than the extra tile traffic).
-constexpr int kPreMinBlocks = 4;
-
-bool use_tiles(const PrefillPlan &pl, int head_dim) { return head_dim == 128 && pl.nbh >= kPreMinBlocks; }
 
 // Workspace: partial states, then (tiles) one head's tile images, 256-byte aligned.
 int64_t tiles_offset(const PrefillPlan &pl, int head_dim) { return (partial_bytes(pl.grid, head_dim) + 255) / 256 * 256; }
@@ -1545,9 +1552,6 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
     char *tiles = static_cast<char *>(workspace) + tiles_offset(pl, head_dim);
     const unsigned npages = static_cast<unsigned>((seq_len + kPage - 1) / kPage);
     a.total = pl.tper;
-    a.grid = std::min(pl.tper, device_cus());
-    if (a.grid >= 8) a.grid -= a.grid % 8;
-    a.xcd_perm = a.grid % 8 == 0 ? 1 : 0;
     a.tiles = tiles;
     for (int h = 0; h < hkv; ++h) {
       a.head0 = h;

@@ -39,6 +39,9 @@ def _oracle(cache, q, row, seq_len, ppb=1, rows=None, scale=None):
 @pytest.mark.parametrize("hkv,d,q_len,seq_len", [
     (4, 128, 1, 1), (4, 128, 7, 300), (4, 128, 64, 64), (4, 128, 100, 1000), (2, 128, 33, 2049),
     (4, 128, 250, 4000), (2, 256, 20, 500), (4, 256, 70, 700), (2, 256, 1, 129),
+    # two KV heads with tile images (four or more row blocks): one launch per
+    # head over its own steps, whose grid sizes the partial states
+    (2, 128, 200, 300), (2, 128, 170, 3000), (2, 128, 700, 9000),
 ])
 def test_prefill_matches_oracle(gpu_ops, hkv, d, q_len, seq_len):
     print("prefill hkv=%d d=%d q=%d seq=%d" % (hkv, d, q_len, seq_len), flush=True)
