@@ -123,33 +123,6 @@ __device__ __forceinline__ int seq_pages(const DecodeArgs &a, int b) {
   return static_cast<int>(n < cap ? n : cap);
 }
 
-// Wave-wide scans of non-negative ints by DPP moves (register to register,
-// a few cycles each; the LDS permutes a shuffle compiles to cost a round trip
-// through the LDS unit per step, and the plan is on the critical path of
-// every work-group's prologue).  Within each 16-lane row, row_shr 1, 2, 4, 8
-// (a lane with no source in its row reads 0); then lane 15 of rows 0 and 2 is
-// added to rows 1 and 3 (row_bcast:15) and lane 31 to rows 2 and 3
-// (row_bcast:31).  All 64 lanes must be active.
-template <bool MAX>
-__device__ __forceinline__ int dpp_step(int x, int y) {
-  return MAX ? max(x, y) : x + y;
-}
-template <bool MAX>
-__device__ __forceinline__ int wave_scan_dpp(int x) {
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false));  // row_shr:1
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false));  // row_shr:2
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false));  // row_shr:4
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false));  // row_shr:8
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false));  // row_bcast:15
-  x = dpp_step<MAX>(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));  // row_bcast:31
-  return x;
-}
-// Sum / max over the wave (x >= 0), the same value in every lane.
-__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_scan_dpp<false>(x), kWave - 1); }
-__device__ __forceinline__ int wave_max(int x) { return __builtin_amdgcn_readlane(wave_scan_dpp<true>(x), kWave - 1); }
-// Inclusive prefix sum over the lanes (x >= 0).
-__device__ __forceinline__ int wave_inclusive_scan(int x) { return wave_scan_dpp<false>(x); }
-
 // Pages per split for this batch (same value in every lane and work-group).
 __device__ int plan_pages_per_split(const DecodeArgs &a, int lane) {
   int total = 0, maxn = 0;

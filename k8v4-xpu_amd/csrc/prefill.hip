@@ -1191,20 +1191,24 @@ __global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, cha
   }
 }
 
-// Finishes the blocks split between work-groups: kMergeSplit work-groups per
-// block (a quarter of its rows each, so a launch fills the chip), two threads
-// per row, D/2 dims each.
-constexpr int kMergeSplit = 4;
+// Finishes the blocks split between work-groups: kMergeSplit work-groups of
+// kMergeThreads per block (a launch then fills the chip), kMergeTPR<D>
+// threads per row, 32 dims each.  The pieces are folded in one pass with an
+// online rescale, their states loaded kMergeU at a time (all loads of a
+// round in flight together: the merge is a chain of round trips, not a
+// bandwidth problem).
+constexpr int kMergeSplit = 8;
+constexpr int kMergeThreads = 128;
+constexpr int kMergeU = 4;
+template <int D>
+constexpr int kMergeTPR = kMergeThreads * kMergeSplit / Tile<D>::ROWS;
 
 // Steps of row blocks 0 .. rb - 1 of one KV head (wave-uniform).
 __device__ __forceinline__ int steps_before_block(const PrefillArgs &a, int rb, int lane) {
   int base = 0;
   for (int r0 = 0; r0 < rb; r0 += 64) {
     const int r = r0 + lane;
-    int n = r < rb ? block_pages(a, r) : 0;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
-    base += n;
+    base += wave_sum(r < rb ? block_pages(a, r) : 0);
   }
   return base;
 }
@@ -1214,44 +1218,66 @@ __device__ __forceinline__ int steps_before_block(const PrefillArgs &a, int rb, 
 // `a` holds the launch's schedule (total, grid) and workspace.
 template <int D>
 __device__ __forceinline__ void merge_block(const PrefillArgs &a, const PrefillArgs &sa, int h, int rb, int start,
-                                            int quarter) {
-  constexpr int R = Tile<D>::ROWS;
+                                            int part) {
+  constexpr int R = Tile<D>::ROWS, TPR = kMergeTPR<D>, DT = D / TPR;  // DT = 32 dims per thread
+  static_assert(DT == 32, "32 dims per merge thread");
   const int n = block_pages(sa, rb);
   const int va = range_owner(a, start), vb = range_owner(a, start + n - 1);
   if (va == vb) return;  // one work-group did the whole block
-  const int lr = quarter * (R / kMergeSplit) + threadIdx.x / 2, half = threadIdx.x % 2;
+  const int lr = part * (R / kMergeSplit) + threadIdx.x / TPR, sub = threadIdx.x % TPR;
   const int row = rb * R + lr;
   if (row >= sa.q_len * 6) return;
-  float M = -INFINITY;
-  for (int v = va; v <= vb; ++v) {
-    const int slot = range_start(a, v) >= start ? 0 : 1;
-    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * R * (D + 2);
-    M = fmaxf(M, pp[R * D + lr]);
-  }
-  float l = 0.f;
-  v4f o[D / 8];
+  float M = -INFINITY, l = 0.f;
+  v4f o[DT / 4];
 #pragma unroll
-  for (int e = 0; e < D / 8; ++e) o[e] = (v4f){0.f, 0.f, 0.f, 0.f};
-  for (int v = va; v <= vb; ++v) {
-    const int slot = range_start(a, v) >= start ? 0 : 1;
-    const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * R * (D + 2);
-    const float m = pp[R * D + lr];
-    if (m == -INFINITY) continue;
-    const float wgt = __builtin_amdgcn_exp2f(m - M);
-    l += wgt * pp[R * D + R + lr];
-    const v4f *src = reinterpret_cast<const v4f *>(pp + lr * D + half * (D / 2));
+  for (int e = 0; e < DT / 4; ++e) o[e] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int v0 = va; v0 <= vb; v0 += kMergeU) {
+    // This round's pieces (past vb: the last piece again, dropped below).
+    float mu[kMergeU], lu[kMergeU];
+    v4f ou[kMergeU][DT / 4];
 #pragma unroll
-    for (int e = 0; e < D / 8; ++e) o[e] += wgt * src[e];
+    for (int u = 0; u < kMergeU; ++u) {
+      const int v = min(v0 + u, vb);
+      const int slot = range_start(a, v) >= start ? 0 : 1;
+      const float *pp = a.ws + (static_cast<int64_t>(v) * 2 + slot) * R * (D + 2);
+      mu[u] = pp[R * D + lr];
+      lu[u] = pp[R * D + R + lr];
+      const v4f *src = reinterpret_cast<const v4f *>(pp + lr * D + sub * DT);
+#pragma unroll
+      for (int e = 0; e < DT / 4; ++e) ou[u][e] = src[e];
+    }
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+      if (v0 + u > vb) mu[u] = -INFINITY;
+      Mn = fmaxf(Mn, mu[u]);
+    }
+    if (Mn == -INFINITY) continue;  // no key seen yet by this row
+    const float keep = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+    l *= keep;
+#pragma unroll
+    for (int e = 0; e < DT / 4; ++e) o[e] *= keep;
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+      // A piece that saw no key of this row (m = -inf) and the repeats past
+      // vb are selected away, not multiplied by zero.
+      const bool on = mu[u] != -INFINITY;
+      const float wgt = __builtin_amdgcn_exp2f(mu[u] - Mn);
+      l = on ? l + wgt * lu[u] : l;
+#pragma unroll
+      for (int e = 0; e < DT / 4; ++e) o[e] = on ? o[e] + wgt * ou[u][e] : o[e];
+    }
+    M = Mn;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int tok = row / 6, qh = h * 6 + row % 6;
-  const int64_t ob = static_cast<int64_t>(tok) * sa.out_tok_stride + static_cast<int64_t>(qh) * D + half * (D / 2);
+  const int64_t ob = static_cast<int64_t>(tok) * sa.out_tok_stride + static_cast<int64_t>(qh) * D + sub * DT;
 #pragma unroll
-  for (int e = 0; e < D / 8; ++e) store_out4(sa.out, sa.out_dtype, ob + 4 * e, o[e] * inv);
+  for (int e = 0; e < DT / 4; ++e) store_out4(sa.out, sa.out_dtype, ob + 4 * e, o[e] * inv);
 }
 
 template <int D>
-__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillArgs a) {
   const int b = blockIdx.x / kMergeSplit;
   const int hl = b / a.nbh, rb = b % a.nbh;
   const int start = hl * a.tper + steps_before_block(a, rb, threadIdx.x % 64);
@@ -1345,7 +1371,7 @@ prefill_batch_kernel(PrefillBatchArgs ba) {
 }
 
 template <int D>
-__global__ __launch_bounds__(2 * Tile<D>::ROWS / kMergeSplit) void prefill_batch_merge_kernel(PrefillBatchArgs ba) {
+__global__ __launch_bounds__(kMergeThreads) void prefill_batch_merge_kernel(PrefillBatchArgs ba) {
   const int b = blockIdx.x / kMergeSplit;
   const int i = batch_find(ba.block0, ba.n, b);
   const PrefillArgs &sa = batch_seq(i);
@@ -1557,7 +1583,7 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
       a.head0 = h;
       prefill_convert_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
       prefill_kernel<128, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(PP::THREADS), 0, s>>>(a);
-      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(a);
+      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(kMergeThreads), 0, s>>>(a);
       const int rc = launch_status("k8v4_prefill_paged");
       if (rc) return rc;
     }
@@ -1571,9 +1597,9 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
   if (rc) return rc;
   const dim3 mgrid(static_cast<unsigned>(pl.nbh * hkv * kMergeSplit));
   if (head_dim == 128)
-    prefill_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(a);
+    prefill_merge_kernel<128><<<mgrid, dim3(kMergeThreads), 0, s>>>(a);
   else
-    prefill_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS / kMergeSplit), 0, s>>>(a);
+    prefill_merge_kernel<256><<<mgrid, dim3(kMergeThreads), 0, s>>>(a);
   return launch_status("k8v4_prefill_paged merge");
 }
 
@@ -1677,10 +1703,10 @@ extern "C" int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_to
     const dim3 mgrid(static_cast<unsigned>(blocks * kMergeSplit));
     if (head_dim == 128) {
       prefill_batch_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<128>::THREADS), 0, s>>>(ba);
-      prefill_batch_merge_kernel<128><<<mgrid, dim3(2 * Tile<128>::ROWS / kMergeSplit), 0, s>>>(ba);
+      prefill_batch_merge_kernel<128><<<mgrid, dim3(kMergeThreads), 0, s>>>(ba);
     } else {
       prefill_batch_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<256>::THREADS), 0, s>>>(ba);
-      prefill_batch_merge_kernel<256><<<mgrid, dim3(2 * Tile<256>::ROWS / kMergeSplit), 0, s>>>(ba);
+      prefill_batch_merge_kernel<256><<<mgrid, dim3(kMergeThreads), 0, s>>>(ba);
     }
     const int rc = launch_status("k8v4_prefill_paged_batch");
     if (rc) return rc;
