@@ -39,6 +39,7 @@
 #include "k8v4_common.h"
 
 #include <algorithm>
+#include <vector>
 
 namespace k8v4 {
 namespace {
@@ -1662,7 +1663,11 @@ extern "C" int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_to
   auto s = static_cast<hipStream_t>(stream);
   // Launches of up to kBatchMax non-empty sequences each, one after another
   // on the stream (each launch reuses the workspace after the previous one).
+  // All of them are planned and checked before the first is enqueued, so a
+  // rejected call launches nothing.
   const int ob = out_dtype == K8V4_F32 ? 4 : 2;
+  std::vector<PrefillBatchArgs> launches;
+  std::vector<int64_t> merge_blocks;
   int i = 0;
   while (i < nseq) {
     PrefillBatchArgs ba{};
@@ -1693,19 +1698,24 @@ extern "C" int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_to
     if (ba.n == 0) break;
     ba.step0[ba.n] = static_cast<int>(steps);
     ba.block0[ba.n] = static_cast<int>(blocks);
-    int64_t grid = std::min<int64_t>(static_cast<int64_t>(device_cus()), std::max<int64_t>(1, steps / kMinSteps));
-    if (grid >= 8) grid -= grid % 8;
+    const int64_t grid = persistent_grid(steps);
     for (int k = 0; k < ba.n; ++k) {
       ba.seq[k].total = static_cast<int>(steps);
       ba.seq[k].grid = static_cast<int>(grid);
       ba.seq[k].xcd_perm = grid % 8 == 0 ? 1 : 0;
     }
-    const dim3 mgrid(static_cast<unsigned>(blocks * kMergeSplit));
+    launches.push_back(ba);
+    merge_blocks.push_back(blocks);
+  }
+  for (size_t j = 0; j < launches.size(); ++j) {
+    const PrefillBatchArgs &ba = launches[j];
+    const dim3 grid(static_cast<unsigned>(ba.seq[0].grid));
+    const dim3 mgrid(static_cast<unsigned>(merge_blocks[j] * kMergeSplit));
     if (head_dim == 128) {
-      prefill_batch_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<128>::THREADS), 0, s>>>(ba);
+      prefill_batch_kernel<128><<<grid, dim3(Tile<128>::THREADS), 0, s>>>(ba);
       prefill_batch_merge_kernel<128><<<mgrid, dim3(kMergeThreads), 0, s>>>(ba);
     } else {
-      prefill_batch_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(Tile<256>::THREADS), 0, s>>>(ba);
+      prefill_batch_kernel<256><<<grid, dim3(Tile<256>::THREADS), 0, s>>>(ba);
       prefill_batch_merge_kernel<256><<<mgrid, dim3(kMergeThreads), 0, s>>>(ba);
     }
     const int rc = launch_status("k8v4_prefill_paged_batch");

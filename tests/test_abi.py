@@ -207,6 +207,14 @@ def test_prefill_batch_host_checks(lib):
     # A workspace smaller than one launch's partial states: K8V4_ERR_WORKSPACE, nothing launched.
     assert _prefill_batch(lib, [0], [5], [100], [0], ws_bytes=1024) == 2
     assert "prefill workspace holds 1024 bytes" in lib.k8v4_last_error().decode()
+    # Eleven sequences are two launches; the second's sequence is too large for
+    # the schedule.  Every launch is planned before the first is enqueued, so
+    # the call fails on the plan (on a host without a GPU an enqueued launch
+    # would have failed first, with a launch error).
+    n, big = 11, (1 << 30) - 1
+    assert _prefill_batch(lib, [0] * n, [5] * (n - 1) + [1 << 20], [100] * (n - 1) + [big], list(range(n)),
+                          ppb=1 << 20, ws_bytes=1 << 30) == 1
+    assert "sequence 10 too large for one call" in lib.k8v4_last_error().decode()
 
 
 def test_prefill_batch_workspace_covers_every_short_single_call(lib):
