@@ -9,10 +9,13 @@ non-contiguous block tables.  Prints ONE JSON line:
 * ``value``: whole-step throughput in GB/s of algorithmic KV bytes
   (4 x 131,072 tokens x 816 B = 427,819,008 B per step), from the wall clock
   around exactly ``--steps`` steps bracketed by device synchronisations;
-* ``roofline``: the split-K kernel alone, timed with HIP events recorded on
-  the stream it runs on (the library records one between its two kernels),
-  against the 8 TB/s HBM peak; ``traffic`` comes from the committed
-  rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
+* ``roofline``: the split-K kernel inside full steps, timed with HIP events
+  on the stream it runs on -- one recorded before each step, one the library
+  records between its split and merge kernels -- over ``--steps`` steps run
+  right after the wall-clock ones, against the 8 TB/s HBM peak
+  (``kernel_us_back_to_back``: the same kernel launched alone, back to back,
+  which starts while the previous launch's stores drain); ``traffic`` comes
+  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
 * ``cpu_baseline``: the reference's PyTorch path restated in torch
   (oracle/torch_cpu.py) on every host core: the whole headline decode step,
   config 2's store and config 5's whole prefill chunk; the float64 oracle
@@ -308,6 +311,26 @@ def kernel_us(torch, hip, work, stages, steps, warmup):
     return us
 
 
+def split_in_step_us(torch, hip, work, steps, warmup):
+    """Average microseconds of the split-K kernel inside full steps (split +
+    merge): an event recorded on the launch stream before each step and one
+    the library records between its two kernels (``split_done``)."""
+    stream = int(torch.cuda.current_stream().cuda_stream)
+    for i in range(warmup):
+        work.launch(i)
+    synchronize(torch)
+    evs = [(hip.create(), hip.create()) for _ in range(steps)]
+    for i, (a, b) in enumerate(evs):
+        hip.record(a, stream)
+        work.launch(warmup + i, split_done=b)
+    synchronize(torch)
+    us = 1e3 * sum(hip.ms(a, b) for a, b in evs) / steps
+    for a, b in evs:
+        hip.destroy(a)
+        hip.destroy(b)
+    return us
+
+
 def graph_us(torch, work, launches=20, replays=10, reps=7):
     """Per-launch microseconds from a HIP graph of ``launches`` back-to-back
     launches (rotating the work's input copies), replayed ``replays`` times
@@ -600,8 +623,9 @@ def main(argv=None) -> int:
     ms_per_step = 1e3 * wall / args.steps
     gbs = work.kv_bytes / (wall / args.steps) / 1e9
 
+    split_us = split_in_step_us(torch, hip, work, args.steps, args.warmup)
     step_graph = graph_us(torch, work)
-    split_us = kernel_us(torch, hip, work, 1, args.steps, args.warmup)
+    split_b2b_us = kernel_us(torch, hip, work, 1, args.steps, args.warmup)
     merge_us = kernel_us(torch, hip, work, 2, args.steps, args.warmup)
     achieved = work.kv_bytes / (split_us * 1e-6) / 1e9
     copy_gbs = copy_peak_gbs(torch, hip)
@@ -641,6 +665,8 @@ def main(argv=None) -> int:
             "traffic": traffic_from_profile(),
             "algorithmic_bytes_per_launch": work.kv_bytes,
             "kernel_us": round(split_us, 2),
+            "kernel_timing": "inside full steps: HIP events before each step and between split and merge",
+            "kernel_us_back_to_back": round(split_b2b_us, 2),
             "merge_kernel_us": round(merge_us, 2),
             "copy_peak_GBps": round(copy_gbs, 1),
             "frac_of_copy_peak": round(achieved / copy_gbs, 4),
