@@ -225,7 +225,10 @@ int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const i
  * (no per-head tile pre-pass), which suits short chunks: a long chunk is
  * faster through k8v4_prefill_paged.  The same bottom-right causal rule,
  * numerics and errors per sequence as k8v4_prefill_paged; q_lens[i] == 0
- * sequences are skipped; nseq == 0 is a no-op.
+ * sequences are skipped; nseq == 0 is a no-op.  The library sees neither
+ * the table's row count nor the token count of q and out: the caller keeps
+ * rows[i] a row of the table and tok0[i] + q_lens[i] within q and out (the
+ * Python op checks both against the tensors' shapes).
  * workspace: >= k8v4_prefill_batch_workspace_bytes(hkv, head_dim) bytes.
  */
 int k8v4_prefill_paged_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
