@@ -30,12 +30,14 @@ extern "C" {
 #endif
 
 /*
- * Version 2: at head dim 256 with two KV heads the decode workspace holds the
- * quantized query tile ahead of the split states, and
- * k8v4_attn_workspace_bytes counts it (a workspace sized as splits x state
- * bytes alone now holds fewer splits).  Version 1: the first release.
+ * Version 3: at head dim 256 with four KV heads too, the decode workspace
+ * holds the quantized query tile ahead of the split states (k8v4_attn_batch
+ * runs every 256-dim cache as paired 128-dim halves).  Version 2: the same
+ * at head dim 256 with two KV heads, and k8v4_attn_workspace_bytes counts it
+ * (a workspace sized as splits x state bytes alone holds fewer splits).
+ * Version 1: the first release.
  */
-#define K8V4_ABI_VERSION 2
+#define K8V4_ABI_VERSION 3
 
 enum {
   K8V4_OK = 0,
@@ -120,7 +122,7 @@ int k8v4_q_quant(const void *q, int q_dtype, int layout, int64_t q_tok_stride, i
  * out: [batch*q_len, 6*hkv, head_dim] of out_dtype, token stride out_tok_stride.
  * workspace: caller-owned device scratch (16-byte aligned) of
  *      workspace_bytes; k8v4_attn_workspace_bytes() gives what a call needs:
- *      the split states and, for head_dim 256 with hkv 2, ahead of them the
+ *      the split states and, for head_dim 256, ahead of them the
  *      query quantized by a first kernel (per sequence and KV head 64 rows of
  *      256 int8 codes, then the rows' fp32 scales).
  * num_splits: split-K work-groups (0 = about one per CU).
@@ -250,7 +252,7 @@ int64_t k8v4_prefill_batch_workspace_bytes(int hkv, int head_dim);
  * k8v4_attn_batch without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * split states (and, at head dim 256 with two KV heads, the quantized query
+ * split states (and, at head dim 256, the quantized query
  * tile ahead of them) go to a library-owned device buffer of
  * k8v4_attn_noalloc_max_bytes() bytes (32 MiB) per GPU, held until the
  * process ends; a call whose k8v4_attn_workspace_bytes exceeds it returns
@@ -270,13 +272,13 @@ int k8v4_attn_batch_noalloc(const void *q, int q_dtype, int64_t q_tok_stride, co
                             int num_splits, void *stream);
 
 /* Bytes of the library-owned buffer of k8v4_attn_batch_noalloc (split states
- * and, at head dim 256 with two KV heads, the query tile). */
+ * and, at head dim 256, the query tile). */
 int64_t k8v4_attn_noalloc_max_bytes(void);
 
 /*
  * Diagnostics, no counterpart in the reference: how many in-kernel waits of
  * the decode kernels on the current device gave up since the library was
- * loaded (the paired-halves handshake of head dim 256 with two KV heads caps
+ * loaded (the paired-halves handshake of head dim 256 caps
  * each wait; a give-up means a wrong output).  Synchronizes with the device
  * (a copy from device memory); -1 on a HIP error.  Zero in a correct run.
  */

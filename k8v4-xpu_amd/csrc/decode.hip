@@ -31,13 +31,13 @@
 //    P.V and the row sums on v_mfma_f32_16x16x32_f16 with fp32 accumulation.
 //  * Each split writes (m, l, O / l in fp16) for its live rows only; a small
 //    merge kernel combines the splits of each output row.
-//  * Head dim 256 with two KV heads runs as paired halves: the cache's rows
-//    are read as those of a 128-dim cache with four heads, two waves per
-//    SIMD; the two waves of a pair score each chunk over both of their K
-//    slots and each accumulates its own 128 output dims (a 256-dim wave needs
-//    all 512 registers of a SIMD lane, so one wave per SIMD, latency-bound).
-//    Its query is quantized by a small kernel ahead of the split kernel, once
-//    for all work-groups.
+//  * Head dim 256 runs as paired halves: the cache's rows are read as those
+//    of a 128-dim cache with twice the heads, two waves per SIMD; the two
+//    waves of a pair score each chunk over both of their K slots and each
+//    accumulates its own 128 output dims (a 256-dim wave needs all 512
+//    registers of a SIMD lane, so one wave per SIMD, latency-bound).  Its
+//    query is quantized by a small kernel ahead of the split kernel, once for
+//    all work-groups.  Every split-kernel instance is 128-dim.
 #include "k8v4_common.h"
 
 #include <cfloat>
@@ -836,7 +836,7 @@ __device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target, int
 template <int D, int NT, bool QLDS, bool RAISE = false>
 __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, const v4i (&sc)[2][NT],
                                                  const lds_t *vslot, int tbase, int L0, int lane, int g,
-                                                 bool masked, const __attribute__((address_space(3))) int *lims) {
+                                                 bool masked) {
   using S = Slot<D>;
   constexpr int DG = S::DG;
   // Phase fences keep the scheduler from hoisting later LDS reads into this
@@ -892,7 +892,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
       for (int ml = 0; ml < 2; ++ml)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (tbase + 16 * ml + 4 * g + i >= (D == 256 ? lims[nt * 16 + (lane & 15)] : st.lim[nt])) t[ml][nt][i] = -INFINITY;
+          if (tbase + 16 * ml + 4 * g + i >= st.lim[nt]) t[ml][nt][i] = -INFINITY;
     }
 #pragma unroll
     for (int ml = 0; ml < 2; ++ml)
@@ -901,13 +901,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
     lmx[nt] = mx;
     // A row's largest score passes the threshold exactly when one of its four
     // lanes' does, so the cross-lane max is only taken on a rescale.
-    // (D = 256 compares in the scaled domain instead of keeping the
-    // thresholds: three fewer registers where the output accumulators take
-    // nearly all of them.)
-    if constexpr (D == 256)
-      grow |= mx * st.crow[nt] > st.m_run[nt] + kRescaleThreshold;
-    else
-      grow |= mx > st.thr[nt];
+    grow |= mx > st.thr[nt];
   }
   if (__ballot(grow)) {
 #pragma unroll
@@ -923,16 +917,12 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
         st.lsum[nt][i] *= ai[i];
         st.corr[nt][i] *= ai[i];
       }
-      // One 16 x 16 accumulator tile at a time (a fence between tiles keeps
-      // the compiler from moving every accumulator through registers at once).
 #pragma unroll
       for (int dg = 0; dg < DG; ++dg)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
           for (int i = 0; i < 4; ++i) st.O[nt][dg][j][i] *= ai[i];
-          if constexpr (D == 256) __builtin_amdgcn_sched_barrier(0);
-        }
     }
   }
   // ---- P = exp2(score * c - m), packed fp16 in the PV A-operand layout; row sums by MFMA
@@ -1028,9 +1018,8 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
 template <int D, int NT, int HKV, int NWH, bool PH = false>
 struct SplitConfig {
   // The int8 Q operands live in LDS with two waves per head (shared by the
-  // pair) and with one wave per head at D = 256 when a two-slot K ring still
-  // fits beside them (held in registers they would be spilled: the 256-dim
-  // output accumulators take most of them); otherwise in registers.  Each
+  // pair) and for paired halves (kept per whole head); otherwise, one wave
+  // per head, in registers.  Each
   // wave owns a K ring of RK slots and a V ring of RV slots, the K ring as
   // deep as the LDS allows; with two waves per SIMD a K slot is refilled as
   // soon as its QK^T product is issued, so while a wave computes one chunk
@@ -1041,13 +1030,11 @@ struct SplitConfig {
   static constexpr int QHEADS = PH ? HKV / 2 : HKV;
   static constexpr int WAVES = HKV * NWH;
   static constexpr int Q_FRAG_BYTES = NT * (DQ / 64) * kWave * 16;        // int8 B-operand fragments
-  // + per-row factors (and at D = 256 the rows' causal ends, kept out of
-  // the registers the 256-dim accumulators fill)
-  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4 * (D == 256 ? 2 : 1);
-  // 4 / HKV work-groups share a CU (the grid is about that many per CU).
-  static constexpr int LDS_MAX = 163840 * HKV / 4;
-  static constexpr bool QLDS =
-      PH || NWH > 1 || (D == 256 && HKV * Q_LDS_BYTES + WAVES * (2 * Slot<D>::K_BYTES + 2 * Slot<D>::V_BYTES) <= LDS_MAX);
+  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4;           // + per-row factors
+  // 4 / HKV work-groups share a CU (the grid is about that many per CU; one
+  // with eight half-head waves).
+  static constexpr int LDS_MAX = HKV >= 4 ? 163840 : 163840 * HKV / 4;
+  static constexpr bool QLDS = PH || NWH > 1;
   static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_LDS_BYTES : 0;
   static constexpr int Q_TOTAL = QHEADS * Q_BYTES_PER_HEAD;
   // PH handshake words: per wave, the chunks whose K half is resident and
@@ -1075,7 +1062,7 @@ struct SplitConfig {
   static constexpr int XCHG_FLOATS = (NT * (D / 128) * 8 * 4 + NT * 4 + NT) * kWave;
   static constexpr int XCHG_BYTES = NWH > 1 ? HKV * XCHG_FLOATS * 4 : 0;
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
-  static constexpr int OCC = NWH;  // waves per SIMD the kernel is built for
+  static constexpr int OCC = HKV > 4 ? HKV * NWH / 4 : NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
   // With two waves per head, the query rows of a wave's tiles are staged in
   // its K slots 1..RK-1.
@@ -1094,9 +1081,10 @@ struct SplitConfig {
 // per row).
 template <int D, int NT, int HKV, int NWH, bool PH = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV * NWH, 64 * HKV * NWH),
-                          amdgpu_waves_per_eu(NWH, NWH)))
+                          amdgpu_waves_per_eu(SplitConfig<D, NT, HKV, NWH, PH>::OCC,
+                                              SplitConfig<D, NT, HKV, NWH, PH>::OCC)))
 void decode_split_kernel(DecodeArgs a) {
-  static_assert(!PH || D == 128, "paired halves are 128-dim");
+  static_assert(D == 128, "split-kernel instances are 128-dim (head dim 256 runs as paired halves)");
   using S = Slot<D>;
   using CFG = SplitConfig<D, NT, HKV, NWH, PH>;
   constexpr int KS = S::KS, DG = S::DG, RK = CFG::RK, RV = CFG::RV;
@@ -1179,13 +1167,6 @@ void decode_split_kernel(DecodeArgs a) {
         if (r < rows && r / kGqa == j) st.lim[nt] = min(e, L0);
       }
     }
-  }
-  // (D = 256: the causal ends live in LDS after the per-row factors.)
-  const auto *lims = reinterpret_cast<const __attribute__((address_space(3))) int *>(qlds + CFG::Q_FRAG_BYTES) + NT * 16;
-  if constexpr (D == 256) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      if (g == 0) const_cast<__attribute__((address_space(3))) int *>(lims)[nt * 16 + n] = st.lim[nt];
   }
 
   // This wave's chunks: x0 + w + k*NWH for k < cnt.
@@ -1302,24 +1283,13 @@ void decode_split_kernel(DecodeArgs a) {
       mv[s] = issued;
     }
   };
-  // One wave per head at D = 256 (query words in registers) fills its
-  // whole ring before it quantizes its three or four 256-dim tiles: a use of
-  // the words here puts the compiler's wait for them (they came with the
-  // table entries) before the ring loads, which are inline assembly it does
-  // not count, so the quantization does not wait for the ring.  Per step
-  // with four 256-dim heads: 4 x 32,768 tokens, q = 7, 81.1 -> 79.8 us;
-  // 4 x 16,384, q = 3, 40.9 -> 40.0 us; 8 x 2,048, q = 1, 19.9 -> 19.3 us.
-  // The 128-dim configurations are as fast or faster with only the first
-  // chunk ahead of the quantization.
-  constexpr bool RING_FIRST = PH || (D == 256 && !QSPLIT);
-  if constexpr (RING_FIRST && !PH) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qraw[nt][ks][0]), "v"(qraw[nt][ks][1]));
-  }
+  // Paired halves stage no query rows in their K slots (the query comes
+  // quantized), so their whole ring goes out at once; the others fill the
+  // rest of theirs after the quantization.  (Issuing the whole ring first,
+  // with the query rows in registers, was neutral at 4 x 131,072 tokens and
+  // 0.1-0.4 us slower per step on short contexts.)
   fill_slot(0);
-  if constexpr (RING_FIRST) {
+  if constexpr (PH) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
   }
@@ -1436,7 +1406,7 @@ void decode_split_kernel(DecodeArgs a) {
 
   // The staged query rows have been read (their values are quantized).
   if constexpr (CFG::QLDS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  if constexpr (!RING_FIRST) {
+  if constexpr (!PH) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
   }
@@ -1533,10 +1503,7 @@ void decode_split_kernel(DecodeArgs a) {
       // The K reads of this slot have completed (their values fed the MFMAs).
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
-      int lane_o = lane;
-      asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1544,17 +1511,14 @@ void decode_split_kernel(DecodeArgs a) {
         if (sk == s) mk[s] = issued;
     }
     if (valid)
-      chunk_softmax_pv<D, NT, CFG::QLDS, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end, lims);
+      chunk_softmax_pv<D, NT, CFG::QLDS, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs);
       // PH: so have the other half's.
       if constexpr (PH) pair_flag_wait(flags + CFG::WAVES + (wave ^ 1), k + 1, lane);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RK) * NWH;
-      int lane_o = lane;
-      asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
-      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo_r, kslot));
+      const uint32_t v = static_cast<uint32_t>(issue_k<D, HKV>(a, page_of(xr), xr, lo, kslot));
       valid_mask = (valid_mask & ~(1u << sk)) | (v << sk);
       issued += S::NK;
 #pragma unroll
@@ -1564,10 +1528,7 @@ void decode_split_kernel(DecodeArgs a) {
     if (k + RV < cnt) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int xr = my0 + (k + RV) * NWH;
-      int lane_o = lane;
-      asm volatile("" : "+v"(lane_o));
-      const LaneOffsets lo_r = D == 256 ? lane_offsets<D, HKV, PH>(a, h, lane_o) : lo;
-      issue_v<D, HKV, PH>(a, page_of(xr), xr, lo_r, lane, vslot);
+      issue_v<D, HKV, PH>(a, page_of(xr), xr, lo, lane, vslot);
       issued += S::NVS;
 #pragma unroll
       for (int s = 0; s < RV; ++s)
@@ -1661,46 +1622,51 @@ void decode_split_kernel(DecodeArgs a) {
   }
 }
 
-template <int D, int NT>
-constexpr int waves_per_head() { return (D == 128 && NT <= 3) ? 2 : 1; }
+// Two waves per 128-dim head with up to three row tiles; one with four.
+template <int NT>
+constexpr int waves_per_head() { return NT <= 3 ? 2 : 1; }
 
-template <int D, int HKV>
+template <int HKV>
 void launch_split(DecodeArgs a, int nt, hipStream_t s) {
   const dim3 grid(a.grid);
   a.tile0 = 0;
-  if (D == 256 && nt == 4) {
-    // Four 256-dim tiles do not fit one wave's registers: two launches of two
-    // tiles each (rows 0-31, then 32-63), writing disjoint rows of the same
-    // split states.
-    decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a);
-    a.tile0 = 2;
-    decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a);
-    return;
-  }
   switch (nt) {
-    case 1: decode_split_kernel<D, 1, HKV, waves_per_head<D, 1>()><<<grid, dim3(64 * HKV * waves_per_head<D, 1>()), 0, s>>>(a); break;
-    case 2: decode_split_kernel<D, 2, HKV, waves_per_head<D, 2>()><<<grid, dim3(64 * HKV * waves_per_head<D, 2>()), 0, s>>>(a); break;
-    case 3: decode_split_kernel<D, 3, HKV, waves_per_head<D, 3>()><<<grid, dim3(64 * HKV * waves_per_head<D, 3>()), 0, s>>>(a); break;
-    default:
-      if constexpr (D == 128)
-        decode_split_kernel<D, 4, HKV, waves_per_head<D, 4>()><<<grid, dim3(64 * HKV * waves_per_head<D, 4>()), 0, s>>>(a);
-      break;
+    case 1: decode_split_kernel<128, 1, HKV, waves_per_head<1>()><<<grid, dim3(64 * HKV * waves_per_head<1>()), 0, s>>>(a); break;
+    case 2: decode_split_kernel<128, 2, HKV, waves_per_head<2>()><<<grid, dim3(64 * HKV * waves_per_head<2>()), 0, s>>>(a); break;
+    case 3: decode_split_kernel<128, 3, HKV, waves_per_head<3>()><<<grid, dim3(64 * HKV * waves_per_head<3>()), 0, s>>>(a); break;
+    default: decode_split_kernel<128, 4, HKV, waves_per_head<4>()><<<grid, dim3(64 * HKV * waves_per_head<4>()), 0, s>>>(a); break;
   }
 }
 
-// Head dim 256 with two KV heads runs as paired halves: four 128-dim
-// half-heads, two waves per SIMD (the 256-dim kernel holds one), from a query
-// quantized by its own small kernel into the workspace.
-bool paired_halves(int hkv, int head_dim) { return head_dim == 256 && hkv == 2; }
+// Head dim 256 runs as paired halves: 2 hkv 128-dim half-heads, two waves
+// per SIMD (the 256-dim kernel holds one), from a query quantized by its own
+// small kernel into the workspace.
+bool paired_halves(int hkv, int head_dim) { return head_dim == 256 && (hkv == 2 || hkv == 4); }
 
-void launch_split_pairs(DecodeArgs a, int nt, hipStream_t s) {
+void launch_split_pairs(DecodeArgs a, int nt, int hkv, hipStream_t s) {
   const dim3 grid(a.grid);
   a.tile0 = 0;
+  if (hkv == 4) {
+    // Eight half-head waves, one each: two per SIMD hold at most three row
+    // tiles, so four run as two launches of two tiles (rows 0-31, then
+    // 32-63) writing disjoint rows of the same split states.
+    switch (nt) {
+      case 1: decode_split_kernel<128, 1, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
+      case 2: decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
+      case 3: decode_split_kernel<128, 3, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
+      default:
+        decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
+        a.tile0 = 2;
+        decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
+        break;
+    }
+    return;
+  }
   switch (nt) {
-    case 1: decode_split_kernel<128, 1, 4, waves_per_head<128, 1>(), true><<<grid, dim3(256 * waves_per_head<128, 1>()), 0, s>>>(a); break;
-    case 2: decode_split_kernel<128, 2, 4, waves_per_head<128, 2>(), true><<<grid, dim3(256 * waves_per_head<128, 2>()), 0, s>>>(a); break;
-    case 3: decode_split_kernel<128, 3, 4, waves_per_head<128, 3>(), true><<<grid, dim3(256 * waves_per_head<128, 3>()), 0, s>>>(a); break;
-    default: decode_split_kernel<128, 4, 4, waves_per_head<128, 4>(), true><<<grid, dim3(256 * waves_per_head<128, 4>()), 0, s>>>(a); break;
+    case 1: decode_split_kernel<128, 1, 4, waves_per_head<1>(), true><<<grid, dim3(256 * waves_per_head<1>()), 0, s>>>(a); break;
+    case 2: decode_split_kernel<128, 2, 4, waves_per_head<2>(), true><<<grid, dim3(256 * waves_per_head<2>()), 0, s>>>(a); break;
+    case 3: decode_split_kernel<128, 3, 4, waves_per_head<3>(), true><<<grid, dim3(256 * waves_per_head<3>()), 0, s>>>(a); break;
+    default: decode_split_kernel<128, 4, 4, waves_per_head<4>(), true><<<grid, dim3(256 * waves_per_head<4>()), 0, s>>>(a); break;
   }
 }
 
@@ -1717,11 +1683,12 @@ int64_t split_state_bytes(int hkv, int q_len, int head_dim) {
   return static_cast<int64_t>(hkv) * q_len * kGqa * (2 * head_dim + 8);
 }
 
-// Split work-groups for one call: about one per CU (a work-group is one wave
-// per KV head at one wave per SIMD), never more than the pages, capped by
-// the workspace and by an explicit request.
+// Split work-groups for one call: about one per CU (two with two 128-dim
+// heads, whose work-groups hold half the waves), never more than the pages,
+// capped by the workspace and by an explicit request.  hkv counts the heads
+// the waves serve (the half-heads of paired halves).
 int64_t choose_grid(int64_t batch, int64_t table_width, int ppb, int hkv, int64_t ws_splits, int requested) {
-  int64_t g = requested > 0 ? requested : static_cast<int64_t>(device_cus()) * (4 / hkv);
+  int64_t g = requested > 0 ? requested : static_cast<int64_t>(device_cus()) * (hkv < 4 ? 4 / hkv : 1);
   const int64_t pages = batch * table_width * ppb;
   if (g > pages) g = pages;
   if (g > ws_splits) g = ws_splits;
@@ -1897,11 +1864,11 @@ int attn_batch(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *q
       a.qs_seq_stride = int64_t(hkv) * kPage;
     }
     if (pairs) {
-      launch_split_pairs(a, nt, s);
-    } else if (head_dim == 128) {
-      if (hkv == 4) launch_split<128, 4>(a, nt, s); else launch_split<128, 2>(a, nt, s);
+      launch_split_pairs(a, nt, hkv, s);
+    } else if (hkv == 4) {
+      launch_split<4>(a, nt, s);
     } else {
-      launch_split<256, 4>(a, nt, s);  // (two heads run as paired halves)
+      launch_split<2>(a, nt, s);
     }
     const int rc = launch_status("k8v4_attn_batch split");
     if (rc) return rc;

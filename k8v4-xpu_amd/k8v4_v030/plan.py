@@ -111,10 +111,11 @@ def split_state_bytes(q_len: int, layout: PageLayout) -> int:
 
 
 def query_tile_bytes(batch: int, layout: PageLayout) -> int:
-    """Workspace head of a 256-dim, two-KV-head decode (its query runs through a
-    quantization kernel first): per sequence and KV head 64 rows of int8 codes,
-    then their fp32 scales, each part rounded up to 256 bytes; 0 otherwise."""
-    if not (layout.head_dim == 256 and layout.hkv == 2):
+    """Workspace head of a 256-dim decode (two or four KV heads: its query runs
+    through a quantization kernel first): per sequence and KV head 64 rows of
+    int8 codes, then their fp32 scales, each part rounded up to 256 bytes; 0
+    otherwise."""
+    if not (layout.head_dim == 256 and layout.hkv in (2, 4)):
         return 0
     rows = int(batch) * layout.hkv * PAGE
     return -(-rows * layout.head_dim // 256) * 256 + -(-rows * 4 // 256) * 256

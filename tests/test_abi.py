@@ -48,7 +48,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
         assert fn is not None
         if name in bound:
             assert len(bound[name]) == nparams, name
-    assert lib.k8v4_abi_version() == 2
+    assert lib.k8v4_abi_version() == 3
 
 
 def _attn(lib, **over):
@@ -106,9 +106,9 @@ def test_workspace_bytes_match_the_python_sizing(lib, hkv, d, q_len, splits):
     got = lib.k8v4_attn_workspace_bytes(1, 4096, 1, q_len, hkv, d, splits)
     head = query_tile_bytes(1, lay)
     assert got == attn_workspace_bytes(splits, q_len, lay) == head + splits * split_state_bytes(q_len, lay)
-    # Only the paired-halves shape (head dim 256, two KV heads) quantizes its
-    # query into the workspace: 64 rows of 256 codes and 64 scales per head.
-    assert head == (2 * 64 * 256 + 512 if (hkv, d) == (2, 256) else 0)
+    # Only the paired-halves shapes (head dim 256) quantize their query into
+    # the workspace: 64 rows of 256 codes and 64 scales per head.
+    assert head == (hkv * (64 * 256 + 256) if d == 256 else 0)
     assert split_state_bytes(q_len, lay) % 16 == 0  # every split state starts 16-byte aligned
     # The grid never has fewer splits than sequences.
     assert lib.k8v4_attn_workspace_bytes(8, 4096, 1, q_len, hkv, d, 3) == attn_workspace_bytes(8, q_len, lay, 8)

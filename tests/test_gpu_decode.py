@@ -312,7 +312,7 @@ def test_explicit_visible_ends_out_of_order(gpu_ops):
     assert_close(out.cpu().numpy(), _oracle(cache, q, table, seq, q_len, visible=vis), what="explicit ends")
 
 
-@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256), (4, 256)])
 def test_zero_length_rows_and_output_dtypes(gpu_ops, hkv, d):
     print("zero-length rows hkv=%d d=%d" % (hkv, d), flush=True)
     lay = PageLayout(hkv, d)
@@ -338,7 +338,7 @@ def test_zero_length_rows_and_output_dtypes(gpu_ops, hkv, d):
     assert assert_close(outbf32.cpu().numpy(), want_bf, what="bf16 q, fp32 out") < 5e-4
 
 
-@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256), (4, 256)])
 def test_values_near_the_fp16_limit_survive_the_split_states(gpu_ops, hkv, d):
     """Every 7th token's V row alternates 60000 / -65504, whose -65504 codes
     dequantize beyond the fp16 range (-8 * 125504 / 15 = -66935), and its K row draws

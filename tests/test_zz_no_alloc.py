@@ -43,10 +43,11 @@ def _both(lib, cache, q, table, seq, q_len):
     return with_ws, no_ws
 
 
-@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256)])
+@pytest.mark.parametrize("hkv,d", [(4, 128), (2, 256), (4, 256)])
 def test_noalloc_entry_matches_the_workspace_entry_on_two_calls(hkv, d):
-    """(4, 128): split states only; (2, 256): the paired-halves layout, whose
-    query tile sits ahead of the split states in the same buffer."""
+    """(4, 128): split states only; (2, 256) and (4, 256): the paired-halves
+    layout, whose query tile sits ahead of the split states in the same
+    buffer."""
     lib = ops_api.load_library()
     print("noalloc hkv=%d d=%d: first call (2 x 20,000, q=7)" % (hkv, d), flush=True)
     lay = PageLayout(hkv, d)
