@@ -24,7 +24,8 @@ non-contiguous block tables.  Prints ONE JSON line:
   graphs of back-to-back launches replayed between two events (median and
   min of several replays), which leaves out the host launch cost;
 * ``configs``: microseconds per layer of the other workloads (store, short
-  decode, MTP verify, mixed long context, prefill, the D=256 per-rank shape).
+  decode, MTP verify, mixed long context, prefill, the D=256 per-rank shape,
+  four 256-dim KV heads).
 
 Inputs are synthetic: fp16 N(0,1) K/V quantized into the cache by the store
 kernel, fp16 N(0,1) queries.  Several copies of each cache are rotated from
@@ -589,6 +590,7 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
         progress("5_prefill_4224_over_131072: %.1f us/layer, %.1f TFLOP/s" % (us, tflops))
     decode_row("reference_shape_d256_hkv2_ctx127853_q7", [127853], 7, copies=4, seed=1007,
                hkv=2, head_dim=256)
+    decode_row("d256_hkv4_4x32768_q7", [32768] * 4, 7, copies=3, seed=1008, hkv=4, head_dim=256)
     return rows
 
 
