@@ -1622,19 +1622,23 @@ void decode_split_kernel(DecodeArgs a) {
   }
 }
 
-// Two waves per 128-dim head with up to three row tiles; one with four.
-template <int NT>
-constexpr int waves_per_head() { return NT <= 3 ? 2 : 1; }
-
+// Two waves per 128-dim head, each holding up to three row tiles: four
+// tiles (q_len 9-10) run as a launch of three (rows 0-47) and one of one
+// (rows 48-63) over the same plan, writing disjoint rows of the same split
+// states; the second launch re-reads pages the first left in the MALL.
 template <int HKV>
 void launch_split(DecodeArgs a, int nt, hipStream_t s) {
-  const dim3 grid(a.grid);
+  const dim3 grid(a.grid), block(128 * HKV);
   a.tile0 = 0;
   switch (nt) {
-    case 1: decode_split_kernel<128, 1, HKV, waves_per_head<1>()><<<grid, dim3(64 * HKV * waves_per_head<1>()), 0, s>>>(a); break;
-    case 2: decode_split_kernel<128, 2, HKV, waves_per_head<2>()><<<grid, dim3(64 * HKV * waves_per_head<2>()), 0, s>>>(a); break;
-    case 3: decode_split_kernel<128, 3, HKV, waves_per_head<3>()><<<grid, dim3(64 * HKV * waves_per_head<3>()), 0, s>>>(a); break;
-    default: decode_split_kernel<128, 4, HKV, waves_per_head<4>()><<<grid, dim3(64 * HKV * waves_per_head<4>()), 0, s>>>(a); break;
+    case 1: decode_split_kernel<128, 1, HKV, 2><<<grid, block, 0, s>>>(a); break;
+    case 2: decode_split_kernel<128, 2, HKV, 2><<<grid, block, 0, s>>>(a); break;
+    case 3: decode_split_kernel<128, 3, HKV, 2><<<grid, block, 0, s>>>(a); break;
+    default:
+      decode_split_kernel<128, 3, HKV, 2><<<grid, block, 0, s>>>(a);
+      a.tile0 = 3;
+      decode_split_kernel<128, 1, HKV, 2><<<grid, block, 0, s>>>(a);
+      break;
   }
 }
 
@@ -1648,25 +1652,29 @@ void launch_split_pairs(DecodeArgs a, int nt, int hkv, hipStream_t s) {
   a.tile0 = 0;
   if (hkv == 4) {
     // Eight half-head waves, one each: two per SIMD hold at most three row
-    // tiles, so four run as two launches of two tiles (rows 0-31, then
-    // 32-63) writing disjoint rows of the same split states.
+    // tiles, so four run as a launch of three (rows 0-47) and one of one
+    // (rows 48-63) writing disjoint rows of the same split states.
     switch (nt) {
       case 1: decode_split_kernel<128, 1, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
       case 2: decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
       case 3: decode_split_kernel<128, 3, 8, 1, true><<<grid, dim3(512), 0, s>>>(a); break;
       default:
-        decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
-        a.tile0 = 2;
-        decode_split_kernel<128, 2, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
+        decode_split_kernel<128, 3, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
+        a.tile0 = 3;
+        decode_split_kernel<128, 1, 8, 1, true><<<grid, dim3(512), 0, s>>>(a);
         break;
     }
     return;
   }
   switch (nt) {
-    case 1: decode_split_kernel<128, 1, 4, waves_per_head<1>(), true><<<grid, dim3(256 * waves_per_head<1>()), 0, s>>>(a); break;
-    case 2: decode_split_kernel<128, 2, 4, waves_per_head<2>(), true><<<grid, dim3(256 * waves_per_head<2>()), 0, s>>>(a); break;
-    case 3: decode_split_kernel<128, 3, 4, waves_per_head<3>(), true><<<grid, dim3(256 * waves_per_head<3>()), 0, s>>>(a); break;
-    default: decode_split_kernel<128, 4, 4, waves_per_head<4>(), true><<<grid, dim3(256 * waves_per_head<4>()), 0, s>>>(a); break;
+    case 1: decode_split_kernel<128, 1, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
+    case 2: decode_split_kernel<128, 2, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
+    case 3: decode_split_kernel<128, 3, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
+    default:
+      decode_split_kernel<128, 3, 4, 2, true><<<grid, dim3(512), 0, s>>>(a);
+      a.tile0 = 3;
+      decode_split_kernel<128, 1, 4, 2, true><<<grid, dim3(512), 0, s>>>(a);
+      break;
   }
 }
 
