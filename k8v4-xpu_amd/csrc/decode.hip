@@ -721,10 +721,10 @@ __device__ __forceinline__ float xlane_max16_32(float x) {
   return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
-template <int D, int NT, bool QLDS>
+// (The int8 query operands live in LDS, shared by the waves of a head.)
+template <int D, int NT>
 struct WaveState {
-  static constexpr int KS = D / 64, DG = D / 128;
-  v4i qb[QLDS ? 1 : NT][KS];  // int8 Q rows as B operands (in LDS when QLDS)
+  static constexpr int DG = D / 128;
   float crow[NT];   // q_scale * log2(e) / sqrt(D), > 0
   int lim[NT];      // causal end of this lane's row (S layout)
   float m_run[NT];  // running max, log2 domain (S layout)
@@ -734,9 +734,8 @@ struct WaveState {
   v4f O[NT][DG][8]; // unnormalized output (O layout)
 };
 
-template <int D, int NT, bool QLDS>
-__device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const lds_t *kslot, const lds_t *qlds,
-                                         int lane, int g, v4i (&sc)[2][NT]) {
+template <int D, int NT>
+__device__ __forceinline__ void chunk_qk(const lds_t *kslot, const lds_t *qlds, int lane, int g, v4i (&sc)[2][NT]) {
   using S = Slot<D>;
   constexpr int KS = S::KS;
   // ---- QK^T, transposed: S[ml][nt] lane (n,g) reg i = score(token 16*ml+4g+i, row 16*nt+n)
@@ -760,11 +759,8 @@ __device__ __forceinline__ void chunk_qk(const WaveState<D, NT, QLDS> &st, const
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      v4i qf;
-      if constexpr (QLDS)
-        qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
-      else
-        qf = st.qb[nt][ks];
+      const v4i qf =
+          *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
 #pragma unroll
       for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
     }
@@ -833,8 +829,8 @@ __device__ __forceinline__ void pair_flag_wait(const lds_int *f, int target, int
 
 // Softmax and P.V of one chunk whose scores chunk_qk produced; reads the V
 // rows and scale planes of the chunk's V slot.
-template <int D, int NT, bool QLDS, bool RAISE = false>
-__device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, const v4i (&sc)[2][NT],
+template <int D, int NT, bool RAISE = false>
+__device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT> &st, const v4i (&sc)[2][NT],
                                                  const lds_t *vslot, int tbase, int L0, int lane, int g,
                                                  bool masked) {
   using S = Slot<D>;
@@ -996,8 +992,8 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<D, NT, QLDS> &st, con
 // O = sum P' * q * 2^-24 (even dims) or 2^-20 (odd dims); the dequantized
 // value is (q - zero) * scale, so the true accumulator is the rescaled sum
 // minus the zero-point correction.
-template <int D, int NT, bool QLDS>
-__device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
+template <int D, int NT>
+__device__ __forceinline__ void finalize_output(WaveState<D, NT> &st) {
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -1017,15 +1013,14 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT, QLDS> &st) {
 
 template <int D, int NT, int HKV, int NWH, bool PH = false>
 struct SplitConfig {
-  // The int8 Q operands live in LDS with two waves per head (shared by the
-  // pair) and for paired halves (kept per whole head); otherwise, one wave
-  // per head, in registers.  Each
-  // wave owns a K ring of RK slots and a V ring of RV slots, the K ring as
-  // deep as the LDS allows; with two waves per SIMD a K slot is refilled as
-  // soon as its QK^T product is issued, so while a wave computes one chunk
-  // up to RK - 1 K slots and RV - 1 V slots are in flight.
-  // Paired halves (PH): D = 128 and HKV half-heads serve a 256-dim cache of
-  // HKV / 2 heads; the query fragments (all 256 dims) are kept per whole head.
+  // Two waves per head (NWH = 2), or paired halves (PH) with one or two
+  // waves per half-head; two waves per SIMD either way.  The int8 Q operands
+  // live in LDS, per head (shared by its waves; PH: all 256 dims, per whole
+  // head).  Each wave owns a K ring of RK slots and a V ring of RV slots,
+  // the K ring as deep as the LDS allows; a K slot is refilled as soon as
+  // its QK^T product is issued, so while a wave computes one chunk up to
+  // RK - 1 K slots and RV - 1 V slots are in flight.  PH: D = 128 and HKV
+  // half-heads serve a 256-dim cache of HKV / 2 heads.
   static constexpr int DQ = PH ? 2 * D : D;       // dims of one score
   static constexpr int QHEADS = PH ? HKV / 2 : HKV;
   static constexpr int WAVES = HKV * NWH;
@@ -1034,8 +1029,7 @@ struct SplitConfig {
   // 4 / HKV work-groups share a CU (the grid is about that many per CU; one
   // with eight half-head waves).
   static constexpr int LDS_MAX = HKV >= 4 ? 163840 : 163840 * HKV / 4;
-  static constexpr bool QLDS = PH || NWH > 1;
-  static constexpr int Q_BYTES_PER_HEAD = QLDS ? Q_LDS_BYTES : 0;
+  static constexpr int Q_BYTES_PER_HEAD = Q_LDS_BYTES;
   static constexpr int Q_TOTAL = QHEADS * Q_BYTES_PER_HEAD;
   // PH handshake words: per wave, the chunks whose K half is resident and
   // the chunks whose K slots it has finished reading.
@@ -1043,11 +1037,9 @@ struct SplitConfig {
   // share a SIMD): one chunk counter per wave.
   static constexpr bool BALANCE = NWH == 2 && WAVES == 8 && !PH;
   static constexpr int FLAG_BYTES = PH ? 2 * WAVES * 4 : (BALANCE ? WAVES * 4 : 0);
-  // One wave per SIMD (NWH == 1) has no partner wave to cover the table
-  // lookup of a mid-chunk refill: it refills its K slot after P.V, next to
-  // the V slot.  So does a PH wave, whose slot the other half of its pair
-  // reads during its own QK^T.
-  static constexpr bool K_EARLY = NWH > 1 && !PH;
+  // A PH wave refills its K slot after P.V, next to the V slot: the other
+  // half of its pair reads that slot during its own QK^T.
+  static constexpr bool K_EARLY = !PH;
   static constexpr int RV = 2;
   static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL - FLAG_BYTES) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
   static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
@@ -1064,9 +1056,9 @@ struct SplitConfig {
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
   static constexpr int OCC = HKV > 4 ? HKV * NWH / 4 : NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
-  // With two waves per head, the query rows of a wave's tiles are staged in
-  // its K slots 1..RK-1.
-  static_assert(NWH == 1 || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
+  static_assert(PH || NWH == 2, "128-dim heads run two waves each");
+  // The query rows of a wave's tiles are staged in its K slots 1..RK-1.
+  static_assert(PH || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
                 "query staging does not fit the K ring");
 };
 
@@ -1121,34 +1113,7 @@ void decode_split_kernel(DecodeArgs a) {
   // and their quantization below.
   const bool pre_q = a.q8 != nullptr;  // uniform over the launch
 
-  // Query tiles this wave quantizes: all NT of them, except when the NWH
-  // waves of a head share their fragments through LDS (tiles w, w + NWH, ...).
-  constexpr bool QSPLIT = CFG::QLDS && NWH > 1;
-
-  // Raw query words.  With Q in registers (one wave per head) they are
-  // loaded here, before the ring's first loads, so they do not wait behind
-  // them (vector loads complete in order); with Q in LDS they are staged by
-  // direct-to-LDS loads further down.
-  v4i qraw[QSPLIT ? 1 : NT][KS][2];
-#pragma unroll
-  for (int nt = 0; nt < (QSPLIT || PH ? 0 : NT); ++nt) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qraw[nt][ks][0] = qraw[nt][ks][1] = (v4i){0, 0, 0, 0};
-    const int r = r0 + 16 * nt + n;
-    if (r < rows && !pre_q) {
-      const int j = r / kGqa;
-      const int qh = h * kGqa + (r - j * kGqa);
-      const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + j) * a.q_tok_stride +
-                            static_cast<int64_t>(qh) * D;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        qraw[nt][ks][0] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g);
-        qraw[nt][ks][1] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g + 8);
-      }
-    }
-  }
-
-  WaveState<D, NT, CFG::QLDS> st;
+  WaveState<D, NT> st;
   lds_t *qlds = lds + CFG::Q_OFF + hq * CFG::Q_BYTES_PER_HEAD;
   // Causal ends, through scalar loads (they are uniform over the
   // work-group): row r (token j = r / 6) sees keys t < lim(r).
@@ -1191,7 +1156,7 @@ void decode_split_kernel(DecodeArgs a) {
   // count of this wave's own loads.  Rows past the last query row load row 0
   // and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if (QSPLIT && !PH && !pre_q) {
+  if (!PH && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
     const char *qbase = reinterpret_cast<const char *>(a.q) + static_cast<int64_t>(b) * a.q_len * a.q_tok_stride * 2;
 #pragma unroll
@@ -1293,11 +1258,11 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
   }
-  if constexpr (QSPLIT || PH) wait_vm(issued - q_done);
+  wait_vm(issued - q_done);
 
   // Q rows of this head -> int8 B operands, quantized with the store's K rule
-  // in float64 (oracle.py:22-40 applied to each query row).  With Q in LDS
-  // each wave quantizes its own tiles (nt % NWH == w) and publishes them.
+  // in float64 (oracle.py:22-40 applied to each query row); each wave
+  // quantizes its own tiles (nt % NWH == w) and publishes them in LDS.
   if constexpr (PH) {
     // Rows past the live ones: zero operands (a caller's tile may hold
     // anything in its padding rows).
@@ -1319,9 +1284,7 @@ void decode_split_kernel(DecodeArgs a) {
     const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + hq * kPage;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      if constexpr (CFG::QLDS) {
-        if (nt % NWH != w) continue;
-      }
+      if (nt % NWH != w) continue;
       const int r = r0 + 16 * nt + n;
       const bool live = r < rows;
 #pragma unroll
@@ -1329,38 +1292,26 @@ void decode_split_kernel(DecodeArgs a) {
         if (PH && (ks >> 1) != half) continue;
         const v4i frag = live ? *reinterpret_cast<const v4i *>(tile + static_cast<int64_t>(r) * DQ + 64 * ks + 16 * g)
                               : (v4i){0, 0, 0, 0};
-        if constexpr (CFG::QLDS) {
-          *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KSQ + ks) * kWave + lane) * 16) = frag;
-        } else {
-          st.qb[nt][ks] = frag;
-        }
+        *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KSQ + ks) * kWave + lane) * 16) = frag;
       }
       const double c = static_cast<double>(live ? scales[r] : 0.f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(DQ)));
       st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
-      if constexpr (CFG::QLDS) {
-        if (g == 0 && half == 0)
-          reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
-      }
+      if (g == 0 && half == 0)
+        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
     }
   } else if constexpr (!PH) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      if (QSPLIT && nt % NWH != w) continue;  // the partner wave quantizes this tile
+      if (nt % NWH != w) continue;  // the partner wave quantizes this tile
       const bool live = r0 + 16 * nt + n < rows;
       float x[KS][16];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const v4i zero = {0, 0, 0, 0};
-        v4i w0, w1;
-        if constexpr (QSPLIT) {
-          const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
-          w0 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row) : zero;
-          w1 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16) : zero;
-        } else {
-          w0 = qraw[nt][ks][0];
-          w1 = qraw[nt][ks][1];
-        }
+        const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
+        const v4i w0 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row) : zero;
+        const v4i w1 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16) : zero;
         const uint32_t words[8] = {static_cast<uint32_t>(w0[0]), static_cast<uint32_t>(w0[1]),
                                    static_cast<uint32_t>(w0[2]), static_cast<uint32_t>(w0[3]),
                                    static_cast<uint32_t>(w1[0]), static_cast<uint32_t>(w1[1]),
@@ -1387,25 +1338,19 @@ void decode_split_kernel(DecodeArgs a) {
           wq[e >> 2] |= (static_cast<uint32_t>(k_rule_code(x[ks][e], inv)) & 0xFFu) << (8 * (e & 3));
         const v4i frag = (v4i){static_cast<int>(wq[0]), static_cast<int>(wq[1]), static_cast<int>(wq[2]),
                                static_cast<int>(wq[3])};
-        if constexpr (CFG::QLDS) {
-          *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16) = frag;
-        } else {
-          st.qb[nt][ks] = frag;
-        }
+        *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16) = frag;
       }
       // score * log2(e) = dot * q_scale * k_scale * log2(e) / sqrt(D); kept > 0
       // so masked (-inf) scores never meet a zero factor.
       const double c = scale * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
       st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
-      if constexpr (CFG::QLDS) {
-        if (g == 0)
-          reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
-      }
+      if (g == 0)
+        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
     }
   }
 
   // The staged query rows have been read (their values are quantized).
-  if constexpr (CFG::QLDS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   if constexpr (!PH) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
@@ -1416,7 +1361,7 @@ void decode_split_kernel(DecodeArgs a) {
     pair_flag_set(flags + wave, 0, lane);
     pair_flag_set(flags + CFG::WAVES + wave, 0, lane);
   }
-  if constexpr (CFG::QLDS) {
+  {
     // Q fragments and row factors visible to both waves of the head.  A bare
     // barrier after the LDS writes: __syncthreads() would also wait for every
     // ring load in flight.
@@ -1497,7 +1442,7 @@ void decode_split_kernel(DecodeArgs a) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       pair_flag_set(flags + CFG::WAVES + wave, k + 1, lane);
     } else {
-      if (valid) chunk_qk<D, NT, CFG::QLDS>(st, kslot, qlds, lane, g, sc);
+      if (valid) chunk_qk<D, NT>(kslot, qlds, lane, g, sc);
     }
     if (CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs).
@@ -1511,7 +1456,7 @@ void decode_split_kernel(DecodeArgs a) {
         if (sk == s) mk[s] = issued;
     }
     if (valid)
-      chunk_softmax_pv<D, NT, CFG::QLDS, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+      chunk_softmax_pv<D, NT, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
     if (!CFG::K_EARLY && k + RK < cnt) {
       // The K reads of this slot have completed (their values fed the MFMAs);
       // PH: so have the other half's.
