@@ -13,10 +13,11 @@
 //    all sequences are cut into runs of P pages that never straddle a
 //    sequence, so a batch of 4 x 128K and a batch of {2K, 32K, 128K, 200K}
 //    both fill the chip.  No host read of the lengths: graph-capturable.
-//  * A work-group holds one or two waves per KV head.  Each wave keeps the
-//    6*q_len query rows of its head (int8-quantized in the prologue, padded to
-//    16-row tiles) as MFMA operands, so each K/V byte is fetched from HBM once
-//    and used for every GQA row.
+//  * A work-group holds two waves per KV head (one per half-head with four
+//    256-dim heads), two per SIMD.  The waves of a head share the 6*q_len
+//    query rows of their head (int8-quantized in the prologue, padded to
+//    16-row tiles, up to three tiles per launch) as MFMA operands in LDS, so
+//    each K/V byte is fetched from HBM once and used for every GQA row.
 //  * Each wave owns a ring of LDS slots filled by direct-to-LDS loads
 //    (global_load_lds, nontemporal for K and V): one slot is one 32-token
 //    chunk of its head (K rows with XOR-swizzled 16-byte chunks, V rows in a
