@@ -82,7 +82,7 @@ struct PrefillArgs {
   int xcd_perm;  // map ids so the work-groups of one XCD take adjacent work (grid % 8 == 0)
   float *ws;     // partial states: [grid][2][rows][D + 2] floats
   int head0;     // KV head of step 0 (a launch covers heads head0 .. head0 + total / tper - 1)
-  const char *tiles;  // head dim 128: dequantized tiles of head head0, [page][PP::BUF] bytes (null: convert in-kernel)
+  const char *tiles;  // dequantized tiles of head head0, [page][PP::BUF] (D = 128) or [page][Tile<256>::TBUF] bytes (null: convert in-kernel)
   void *out;
   int out_dtype;
   int64_t out_tok_stride;  // elements
@@ -121,6 +121,11 @@ struct Tile {
   static constexpr int VDMA = D / 32;                 // 1 KB V pieces per page
   static constexpr int KCHUNKS = 4 * D;               // 16-byte K code chunks per page
   static constexpr int VITEMS = 2 * D;                // (part, half, key pair) V items per page
+  // Tile images dequantized beforehand (D = 256): one per page in the
+  // workspace, BUF rounded up to whole 1 KB pieces, each piece one DMA of a
+  // wave; the ring then holds two such images.
+  static constexpr int TBUF = (BUF + 1023) / 1024 * 1024;
+  static constexpr int TPIECES = TBUF / 1024;
 };
 
 typedef const __attribute__((address_space(4))) int32_t *const_i32_ptr;
@@ -318,10 +323,16 @@ __device__ __forceinline__ int range_owner(const PrefillArgs &a, int s) {
 
 // One segment: pages [p_lo, p_hi) of row block rb of KV head h.  `part` is
 // null when the segment is the whole block (the output is written directly).
-template <int D>
+//
+// PRE (D = 256): the pages' tile images were dequantized beforehand
+// (prefill_convert256_kernel writes each page's image to a.tiles once for
+// all row blocks of the head): the ring's two buffers (TBUF apart) receive
+// them by DMA, and the waves only multiply.
+template <int D, bool PRE = false>
 __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, int h, int rb, int p_lo, int p_hi,
                                             float *part, int tid, int wave, int lane) {
   using T = Tile<D>;
+  constexpr int RB = PRE ? T::TBUF : T::BUF;  // ring buffer stride
   lds_t *stage_lds = (lds_t *)(smem + 2 * T::BUF);
   const char *stage = smem + 2 * T::BUF;
   const int nrows = a.q_len * 6;
@@ -376,17 +387,37 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
   const int k_base = r32 * T::KROW + 16 * hh;
   const int v_base = T::V_OFF + r32 * T::VROW + 16 * hh;
 
-  stage_page<D>(a, p_lo, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
-  wait_dma();
-  __syncthreads();
-  convert_page<D>(a, p_lo, stage, smem, tid);
-  __syncthreads();
+  // PRE: wave w moves pieces w, w + NW, ... of a page's image.
+  auto tile_dma = [&](int p, int bi) {
+    const char *src = a.tiles + static_cast<int64_t>(p) * T::TBUF + 16 * lane;
+#pragma unroll
+    for (int j = 0; j < (T::TPIECES + T::NW - 1) / T::NW; ++j) {
+      const int k = T::NW * j + wave;
+      if (k < T::TPIECES) dma16(src + 1024 * k, (lds_t *)(smem + bi * RB + 1024 * k));
+    }
+  };
+  if constexpr (PRE) {
+    tile_dma(p_lo, 0);
+    wait_dma();
+    __syncthreads();
+  } else {
+    stage_page<D>(a, p_lo, h, wave, lane, stage_lds, (lds_t *)(smem + T::S_OFF));
+    wait_dma();
+    __syncthreads();
+    convert_page<D>(a, p_lo, stage, smem, tid);
+    __syncthreads();
+  }
 
   for (int p = p_lo; p < p_hi; ++p) {
     const int bi = (p - p_lo) & 1;
-    const char *buf = smem + bi * T::BUF;
+    const char *buf = smem + bi * RB;
     const bool more = p + 1 < p_hi;
-    if (more) stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + (bi ^ 1) * T::BUF + T::S_OFF));
+    if (more) {
+      if constexpr (PRE)
+        tile_dma(p + 1, bi ^ 1);
+      else
+        stage_page<D>(a, p + 1, h, wave, lane, stage_lds, (lds_t *)(smem + (bi ^ 1) * T::BUF + T::S_OFF));
+    }
 
     // ---- S^T = K Q^T - m for the 64 keys of page p: lane (r, hh) reg 4j+i
     // of tile mt holds key 32*mt + 8*j + 4*hh + i of row r.  The accumulators
@@ -487,8 +518,10 @@ __device__ __forceinline__ void run_segment(const PrefillArgs &a, char *smem, in
 
     if (more) {
       wait_dma();
-      __syncthreads();
-      convert_page<D>(a, p + 1, stage, smem + (bi ^ 1) * T::BUF, tid);
+      if constexpr (!PRE) {
+        __syncthreads();
+        convert_page<D>(a, p + 1, stage, smem + (bi ^ 1) * T::BUF, tid);
+      }
     }
     __syncthreads();
   }
@@ -1112,7 +1145,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(Tile<D>::THREADS, Tile<D>:
                           amdgpu_waves_per_eu(Tile<D>::WPE, Tile<D>::WPE))) void
 prefill_kernel(PrefillArgs a) {
   using T = Tile<D>;
-  constexpr int LDS_BYTES = D == 128 ? PP::LDS : 2 * T::BUF + T::STAGE;
+  constexpr int LDS_BYTES = D == 128 ? PP::LDS : (PRE ? 2 * T::TBUF : 2 * T::BUF + T::STAGE);
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
   const int w = blockIdx.x;
   const int v = a.xcd_perm ? (w % 8) * (a.grid / 8) + w / 8 : w;
@@ -1141,7 +1174,7 @@ prefill_kernel(PrefillArgs a) {
     if constexpr (D == 128)
       run_segment_pp<PRE>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     else
-      run_segment<D>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
+      run_segment<D, PRE>(a, smem, h, rb, p_lo, p_hi, part, tid, wave, lane);
     s += p_hi - p_lo;
     first = false;
   }
@@ -1190,6 +1223,28 @@ __global__ __launch_bounds__(256) void prefill_convert_kernel(PrefillArgs a, cha
     const PPLane L = pp_lane(a, t, 0, r, 0);
     pp_emit_v<true>(a, p, pp_fetch_v(st, L), buf, L);
   }
+}
+
+// D = 256: every page of KV head h dequantized once into its tile image (the
+// LDS layout run_segment multiplies from), one work-group of four waves per
+// page: the page is staged and converted exactly as the attention kernel
+// does in place, then the image leaves LDS with nontemporal 16-byte stores
+// (TBUF bytes: the tail past BUF carries staged codes nothing reads).
+__global__ __launch_bounds__(256) void prefill_convert256_kernel(PrefillArgs a, char *tiles, int h) {
+  using T = Tile<256>;
+  static_assert(T::THREADS == 256 && T::TBUF <= T::BUF + T::STAGE, "one page per work-group of four waves");
+  __shared__ __attribute__((aligned(16))) char smem[T::BUF + T::STAGE];
+  const int p = blockIdx.x, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+  stage_page<256>(a, p, h, wave, lane, (lds_t *)(smem + T::BUF), (lds_t *)(smem + T::S_OFF));
+  wait_dma();
+  __syncthreads();
+  convert_page<256>(a, p, smem + T::BUF, smem, tid);
+  __syncthreads();
+  char *dst = tiles + static_cast<int64_t>(p) * T::TBUF;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  for (int o = 16 * tid; o < T::TBUF; o += 16 * T::THREADS)
+    tile_store<true>(dst + o, *reinterpret_cast<const u32x4 *>(smem + o));
 }
 
 // Finishes the blocks split between work-groups: kMergeSplit work-groups of
@@ -1404,7 +1459,8 @@ int rows_per_block(int head_dim) { return head_dim == 128 ? Tile<128>::ROWS : Ti
 // in-kernel conversion costs less than the extra tile traffic).
 constexpr int kPreMinBlocks = 4;
 
-bool use_tiles(const PrefillPlan &pl, int head_dim) { return head_dim == 128 && pl.nbh >= kPreMinBlocks; }
+bool use_tiles(const PrefillPlan &pl, int head_dim) { return pl.nbh >= kPreMinBlocks; }
+int64_t tile_stride(int head_dim) { return head_dim == 128 ? PP::BUF : Tile<256>::TBUF; }
 
 // Persistent work-groups for a launch of `steps` page steps: one per CU, each
 // with at least kMinSteps steps (a work-group's fixed work -- its query rows,
@@ -1444,7 +1500,7 @@ int64_t partial_bytes(int grid, int head_dim) {
 int64_t tiles_offset(const PrefillPlan &pl, int head_dim) { return (partial_bytes(pl.grid, head_dim) + 255) / 256 * 256; }
 int64_t workspace_need(const PrefillPlan &pl, int64_t seq_len, int head_dim) {
   if (!use_tiles(pl, head_dim)) return partial_bytes(pl.grid, head_dim);
-  return tiles_offset(pl, head_dim) + (seq_len + kPage - 1) / kPage * PP::BUF;
+  return tiles_offset(pl, head_dim) + (seq_len + kPage - 1) / kPage * tile_stride(head_dim);
 }
 
 
@@ -1582,9 +1638,15 @@ extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stri
     a.tiles = tiles;
     for (int h = 0; h < hkv; ++h) {
       a.head0 = h;
-      prefill_convert_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
-      prefill_kernel<128, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(PP::THREADS), 0, s>>>(a);
-      prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(kMergeThreads), 0, s>>>(a);
+      if (head_dim == 128) {
+        prefill_convert_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
+        prefill_kernel<128, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(PP::THREADS), 0, s>>>(a);
+        prefill_merge_kernel<128><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(kMergeThreads), 0, s>>>(a);
+      } else {
+        prefill_convert256_kernel<<<dim3(npages), dim3(256), 0, s>>>(a, tiles, h);
+        prefill_kernel<256, true><<<dim3(static_cast<unsigned>(a.grid)), dim3(Tile<256>::THREADS), 0, s>>>(a);
+        prefill_merge_kernel<256><<<dim3(static_cast<unsigned>(pl.nbh * kMergeSplit)), dim3(kMergeThreads), 0, s>>>(a);
+      }
       const int rc = launch_status("k8v4_prefill_paged");
       if (rc) return rc;
     }

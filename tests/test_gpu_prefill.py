@@ -42,6 +42,8 @@ def _oracle(cache, q, row, seq_len, ppb=1, rows=None, scale=None):
     # two KV heads with tile images (four or more row blocks): one launch per
     # head over its own steps, whose grid sizes the partial states
     (2, 128, 200, 300), (2, 128, 170, 3000), (2, 128, 700, 9000),
+    # head dim 256 with tile images (four or more 128-row blocks)
+    (2, 256, 200, 3000), (2, 256, 700, 9000), (4, 256, 90, 5000),
 ])
 def test_prefill_matches_oracle(gpu_ops, hkv, d, q_len, seq_len):
     print("prefill hkv=%d d=%d q=%d seq=%d" % (hkv, d, q_len, seq_len), flush=True)
