@@ -25,7 +25,7 @@ non-contiguous block tables.  Prints ONE JSON line:
   min of several replays), which leaves out the host launch cost;
 * ``configs``: microseconds per layer of the other workloads (store, short
   decode, MTP verify, mixed long context, prefill, the D=256 per-rank shape,
-  four 256-dim KV heads).
+  four 256-dim KV heads, prefill at the D=256 per-rank shape).
 
 Inputs are synthetic: fp16 N(0,1) K/V quantized into the cache by the store
 kernel, fp16 N(0,1) queries.  Several copies of each cache are rotated from
@@ -569,28 +569,36 @@ def config_rows(torch, hip, ops, steps, warmup, only=None):
     decode_row("3_mtp_verify_4x8192_q7", [8192] * 4, 7, copies=12, seed=1003, pool_pages_per_copy=1024)
     decode_row("4_mixed_long_q7", [2048, 32768, 131072, 200000], 7, copies=3, seed=1004,
                shared_prefix_pages=1024)
-    if want("5_prefill_4224_over_131072"):
-        w = PrefillWorkload(ops, torch)
+    def prefill_row(name, hkv, head_dim, dtype, graph=True):
+        if not want(name):
+            return
+        w = PrefillWorkload(ops, torch, hkv=hkv, head_dim=head_dim)
         warm_clocks(torch, w, 1.0)
         us = kernel_us(torch, hip, w, 3, max(5, steps // 10), 2)
-        g_med, g_min = graph_us(torch, w, launches=2, replays=2, reps=3)
         tflops = w.flops / (us * 1e-6) / 1e12
-        rows["5_prefill_4224_over_131072"] = {
-            "us_per_layer": round(us, 1),
-            "graph_us_median": round(g_med, 1),
-            "graph_us_min": round(g_min, 1),
+        rows[name] = {"us_per_layer": round(us, 1)}
+        if graph:
+            g_med, g_min = graph_us(torch, w, launches=2, replays=2, reps=3)
+            rows[name].update({"graph_us_median": round(g_med, 1), "graph_us_min": round(g_min, 1)})
+        rows[name].update({
             "algorithmic_flops": w.flops,
             "TFLOPs": round(tflops, 1),
             "mfma_peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
             "mfma_utilization": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "dtype": "f16 MFMA (fp16 tiles: K code x k_scale, V (nibble - v_zero) x v_scale / 16), f32 accumulation",
-        }
+            "dtype": dtype,
+        })
         del w
         torch.cuda.empty_cache()
-        progress("5_prefill_4224_over_131072: %.1f us/layer, %.1f TFLOP/s" % (us, tflops))
+        progress("%s: %.1f us/layer, %.1f TFLOP/s" % (name, us, tflops))
+
+    prefill_row("5_prefill_4224_over_131072", 4, 128,
+                "f16 MFMA (fp16 tiles: K code x k_scale, V (nibble - v_zero) x v_scale / 16), f32 accumulation")
     decode_row("reference_shape_d256_hkv2_ctx127853_q7", [127853], 7, copies=4, seed=1007,
                hkv=2, head_dim=256)
     decode_row("d256_hkv4_4x32768_q7", [32768] * 4, 7, copies=3, seed=1008, hkv=4, head_dim=256)
+    prefill_row("prefill_d256_hkv2_4224_over_131072", 2, 256,
+                "f16 MFMA (fp16 tiles: K code x k_scale, V nibbles as fp16 subnormals), f32 accumulation",
+                graph=False)
     return rows
 
 
