@@ -1445,6 +1445,7 @@ namespace {
 
 struct PrefillPlan {
   int nbh, tper, total, grid;
+  bool tiles;  // pages dequantized once per KV head into tile images
 };
 
 // Fewest page steps per persistent work-group when a call has few (one
@@ -1459,7 +1460,17 @@ int rows_per_block(int head_dim) { return head_dim == 128 ? Tile<128>::ROWS : Ti
 // in-kernel conversion costs less than the extra tile traffic).
 constexpr int kPreMinBlocks = 4;
 
-bool use_tiles(const PrefillPlan &pl, int head_dim) { return pl.nbh >= kPreMinBlocks; }
+// Head dim 256 (one wave per SIMD, whose conversion is cheaper in place): per
+// KV head the tile path costs about 59 us of launches and pre-pass latency
+// plus 62 ns per page and saves about 9 ns per (row block, page) -- measured
+// against the in-place conversion over contexts of 4K-64K tokens and chunks
+// of 96-4,224 tokens (two heads; per head either way).
+bool tiles_pay_off(int64_t nbh, int64_t npages, int head_dim) {
+  if (nbh < kPreMinBlocks) return false;
+  return head_dim == 128 || (9 * nbh - 62) * npages > 58600;
+}
+
+bool use_tiles(const PrefillPlan &pl, int /*head_dim*/) { return pl.tiles; }
 int64_t tile_stride(int head_dim) { return head_dim == 128 ? PP::BUF : Tile<256>::TBUF; }
 
 // Persistent work-groups for a launch of `steps` page steps: one per CU, each
@@ -1486,6 +1497,7 @@ bool plan_prefill(int64_t seq_len, int64_t q_len, int hkv, int head_dim, Prefill
   pl.nbh = static_cast<int>(nbh);
   pl.tper = static_cast<int>(tper);
   pl.total = static_cast<int>(total);
+  pl.tiles = tiles_pay_off(nbh, (seq_len + kPage - 1) / kPage, head_dim);
   // The grid of the launch that runs: one per KV head over its tper steps
   // with tile images, else one over all heads.
   pl.grid = static_cast<int>(persistent_grid(use_tiles(pl, head_dim) ? tper : total));

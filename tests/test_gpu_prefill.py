@@ -42,7 +42,8 @@ def _oracle(cache, q, row, seq_len, ppb=1, rows=None, scale=None):
     # two KV heads with tile images (four or more row blocks): one launch per
     # head over its own steps, whose grid sizes the partial states
     (2, 128, 200, 300), (2, 128, 170, 3000), (2, 128, 700, 9000),
-    # head dim 256 with tile images (four or more 128-row blocks)
+    # head dim 256 with several row blocks (converted in place: the tile
+    # images pay off only for longer chunks over longer contexts)
     (2, 256, 200, 3000), (2, 256, 700, 9000), (4, 256, 90, 5000),
 ])
 def test_prefill_matches_oracle(gpu_ops, hkv, d, q_len, seq_len):
@@ -167,6 +168,37 @@ def test_prefill_chunk_4224_over_131072_all_rows(gpu_ops):
         # The CPU port agrees with the float64 oracle on the same rows.
         assert np.abs(want_all[part] - want).max() <= 2e-5
     print("  %d x 24 rows max abs err %.2e; %d rows vs float64 %.2e" % (q_len, err_all, rows.size, err), flush=True)
+
+
+@pytest.mark.parametrize("hkv,q_len,seq_len", [(2, 1500, 7000), (4, 1400, 8000)])
+def test_prefill_d256_over_tile_images_all_rows(gpu_ops, hkv, q_len, seq_len):
+    """Head dim 256 with enough row blocks and pages for the per-head tile
+    images (the workspace holds them: one 68 KB image per page).  Every row
+    against the torch restatement of the reference's prefill, the first and
+    last token of every 128-row block against the float64 oracle; max-abs
+    2e-3 with a 1e-2 relative allowance."""
+    from oracle import torch_cpu
+    from oracle.paged import Geometry
+
+    print("prefill d=256 tiles hkv=%d q=%d seq=%d" % (hkv, q_len, seq_len), flush=True)
+    pages = -(-seq_len // PAGE)
+    assert gpu_ops.prefill_workspace_bytes(seq_len, q_len, hkv, 256) > pages * 68 * 1024
+    lay = PageLayout(hkv, 256)
+    gen = torch.Generator().manual_seed(q_len + seq_len + hkv)
+    cache = Cache(pages + 8, lay)
+    table = random_tables(gen, [seq_len], pages + 8)
+    fill_sequence(gpu_ops, cache, gen, table[0], seq_len)
+    q = seeded_normal(gen, (q_len, lay.hq, 256))
+    got = _run(cache, q, table[0], seq_len, out_dtype=torch.float32).cpu().numpy()
+    views = torch_cpu.region_views(torch.from_numpy(cache.blob().copy()), Geometry(hkv, 256))
+    want_all = torch_cpu.prefill(views, q, table[0].long(), seq_len, 1.0 / math.sqrt(256)).numpy()
+    err_all = assert_close(got, want_all, what="d256 tiles all rows")
+    blocks = (q_len * 6 + 127) // 128
+    rows = np.array(sorted({min(q_len - 1, (128 * k) // 6) for k in range(blocks)} |
+                           {min(q_len - 1, (128 * k + 127) // 6) for k in range(blocks)}))
+    want = _oracle(cache, q, table[0], seq_len, rows=rows)
+    err = assert_close(got[rows], want, what="d256 tiles float64 rows")
+    print("  all rows %.2e, %d rows vs float64 %.2e" % (err_all, rows.size, err), flush=True)
 
 
 @pytest.mark.parametrize("q_len,seq_len", [(3, 5000), (1, 64), (40, 40), (500, 9000)])
