@@ -41,7 +41,7 @@ from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_b
 from vllm.v1.kv_cache_interface import AttentionSpec
 
 from .cache_views import bind_regions
-from .layout import CACHE_DTYPE, DECODE_MAX_T, GQA, PAGE, PageLayout, attention_pages_per_block
+from .layout import CACHE_DTYPE, DECODE_MAX_T, PAGE, PageLayout, attention_pages_per_block
 from .ops_api import ops
 from .plan import layout_for_heads, query_segments, require_decoder, scratch_capacity, token_span, uniform_packed_q_len
 from .scratch import Scratch, ensure_scratch, get_scratch, scratch_ready
@@ -287,11 +287,12 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
             self._decode(q, out, regions, meta, run, scratch)
         if meta.prefill_seqs:
             lens = meta.seq_lens_cpu if meta.seq_lens_cpu is not None else meta.seq_lens.detach().cpu()
-            short = [seq for seq in meta.prefill_seqs if _batched_prefill(seq.width, lay.head_dim)]
+            alone = [_runs_alone(seq.width, int(lens[seq.req]), lay) for seq in meta.prefill_seqs]
+            short = [seq for seq, a in zip(meta.prefill_seqs, alone) if not a]
             if short:
                 self._prefill_batch(q, out, regions, meta, short, lens, scratch)
-            for seq in meta.prefill_seqs:
-                if not _batched_prefill(seq.width, lay.head_dim):
+            for seq, a in zip(meta.prefill_seqs, alone):
+                if a:
                     self._prefill(q, out, regions, meta, seq, int(lens[seq.req]), scratch)
         return output
 
@@ -342,15 +343,16 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
 
 # ----------------------------------------------------------------- helpers
 # Chunks the single prefill entry would run with its in-kernel page conversion
-# (at head dim 128, up to three row blocks of 256 query rows: 128 tokens; at
-# head dim 256 always) gain nothing from running alone: a step's share one
-# batched launch.  Longer chunks at head dim 128 keep the entry that
-# dequantizes each page once per KV head.
-_BATCHED_PREFILL_TOKENS_D128 = 3 * 256 // GQA
-
-
-def _batched_prefill(width: int, head_dim: int) -> bool:
-    return head_dim == 256 or width <= _BATCHED_PREFILL_TOKENS_D128
+# gain nothing from running alone: a step's share one batched launch.  A chunk
+# the single entry serves from per-head tile images (each page dequantized
+# once per KV head: at head dim 128 over 128 tokens; at head dim 256 long
+# chunks over long contexts) runs alone.  The library's plan decides; its
+# workspace shows the choice (tile images beyond the batched launch's
+# partial states).
+def _runs_alone(width: int, seq_len: int, layout) -> bool:
+    o = ops()
+    return (o.prefill_workspace_bytes(seq_len, width, layout.hkv, layout.head_dim)
+            > o.prefill_batch_workspace_bytes(layout.hkv, layout.head_dim))
 
 
 def _check_covers(seq_len: int, width: int) -> None:
