@@ -735,7 +735,9 @@ struct WaveState {
   v4f O[NT][DG][8]; // unnormalized output (O layout)
 };
 
-template <int D, int NT>
+// TS: LDS tiles between this wave's query tiles (2 when the waves of a head
+// hold alternate row tiles).
+template <int D, int NT, int TS = 1>
 __device__ __forceinline__ void chunk_qk(const lds_t *kslot, const lds_t *qlds, int lane, int g, v4i (&sc)[2][NT]) {
   using S = Slot<D>;
   constexpr int KS = S::KS;
@@ -761,7 +763,7 @@ __device__ __forceinline__ void chunk_qk(const lds_t *kslot, const lds_t *qlds, 
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const v4i qf =
-          *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * KS + ks) * kWave + lane) * 16);
+          *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(qlds + ((nt * TS * KS + ks) * kWave + lane) * 16);
 #pragma unroll
       for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
     }
@@ -1012,7 +1014,7 @@ __device__ __forceinline__ void finalize_output(WaveState<D, NT> &st) {
       }
 }
 
-template <int D, int NT, int HKV, int NWH, bool PH = false>
+template <int D, int NT, int HKV, int NWH, bool PH = false, bool RS = false>
 struct SplitConfig {
   // Two waves per head (NWH = 2), or paired halves (PH) with one or two
   // waves per half-head; two waves per SIMD either way.  The int8 Q operands
@@ -1021,12 +1023,16 @@ struct SplitConfig {
   // the K ring as deep as the LDS allows; a K slot is refilled as soon as
   // its QK^T product is issued, so while a wave computes one chunk up to
   // RK - 1 K slots and RV - 1 V slots are in flight.  PH: D = 128 and HKV
-  // half-heads serve a 256-dim cache of HKV / 2 heads.
+  // half-heads serve a 256-dim cache of HKV / 2 heads.  RS (row split, four
+  // row tiles): the two waves of a head hold alternate row tiles (NT each)
+  // and both multiply every chunk of the split, each chunk resident in the
+  // ring of the wave that loaded it.
+  static constexpr int NTQ = RS ? 2 * NT : NT;    // row tiles of a head's query
   static constexpr int DQ = PH ? 2 * D : D;       // dims of one score
   static constexpr int QHEADS = PH ? HKV / 2 : HKV;
   static constexpr int WAVES = HKV * NWH;
-  static constexpr int Q_FRAG_BYTES = NT * (DQ / 64) * kWave * 16;        // int8 B-operand fragments
-  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NT * 16 * 4;           // + per-row factors
+  static constexpr int Q_FRAG_BYTES = NTQ * (DQ / 64) * kWave * 16;       // int8 B-operand fragments
+  static constexpr int Q_LDS_BYTES = Q_FRAG_BYTES + NTQ * 16 * 4;          // + per-row factors
   // 4 / HKV work-groups share a CU (the grid is about that many per CU; one
   // with eight half-head waves).
   static constexpr int LDS_MAX = HKV >= 4 ? 163840 : 163840 * HKV / 4;
@@ -1036,11 +1042,11 @@ struct SplitConfig {
   // the chunks whose K slots it has finished reading.
   // Progress balance (two waves per head, eight waves: waves w and w + 4
   // share a SIMD): one chunk counter per wave.
-  static constexpr bool BALANCE = NWH == 2 && WAVES == 8 && !PH;
-  static constexpr int FLAG_BYTES = PH ? 2 * WAVES * 4 : (BALANCE ? WAVES * 4 : 0);
+  static constexpr bool BALANCE = NWH == 2 && WAVES == 8 && !PH && !RS;
+  static constexpr int FLAG_BYTES = (PH || RS) ? 2 * WAVES * 4 : (BALANCE ? WAVES * 4 : 0);
   // A PH wave refills its K slot after P.V, next to the V slot: the other
   // half of its pair reads that slot during its own QK^T.
-  static constexpr bool K_EARLY = !PH;
+  static constexpr bool K_EARLY = !PH && !RS;
   static constexpr int RV = 2;
   static constexpr int RK_FIT = ((LDS_MAX - Q_TOTAL - FLAG_BYTES) / WAVES - RV * Slot<D>::V_BYTES) / Slot<D>::K_BYTES;
   static constexpr int RK = RK_FIT < 2 ? 2 : (RK_FIT > 4 ? 4 : RK_FIT);
@@ -1053,13 +1059,15 @@ struct SplitConfig {
   static constexpr int RING_BYTES = FLAG_OFF + FLAG_BYTES;
   // Partner-wave state exchange at the end (reuses the ring memory).
   static constexpr int XCHG_FLOATS = (NT * (D / 128) * 8 * 4 + NT * 4 + NT) * kWave;
-  static constexpr int XCHG_BYTES = NWH > 1 ? HKV * XCHG_FLOATS * 4 : 0;
+  static constexpr int XCHG_BYTES = (NWH > 1 && !RS) ? HKV * XCHG_FLOATS * 4 : 0;
   static constexpr int LDS_BYTES = RING_BYTES > XCHG_BYTES ? RING_BYTES : XCHG_BYTES;
   static constexpr int OCC = HKV > 4 ? HKV * NWH / 4 : NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
   static_assert(PH || NWH == 2, "128-dim heads run two waves each");
-  // The query rows of a wave's tiles are staged in its K slots 1..RK-1.
-  static_assert(PH || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
+  static_assert(!RS || (!PH && NWH == 2), "row split: two waves per 128-dim head");
+  // The query rows of a wave's tiles are staged in its K slots 1..RK-1 (RS:
+  // loaded into registers instead).
+  static_assert(PH || RS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
                 "query staging does not fit the K ring");
 };
 
@@ -1072,14 +1080,14 @@ struct SplitConfig {
 // against the DMAs), run the same softmax and accumulate P.V over their own
 // 128 output dims.  The query comes pre-quantized (256-dim rows, one scale
 // per row).
-template <int D, int NT, int HKV, int NWH, bool PH = false>
+template <int D, int NT, int HKV, int NWH, bool PH = false, bool RS = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * HKV * NWH, 64 * HKV * NWH),
-                          amdgpu_waves_per_eu(SplitConfig<D, NT, HKV, NWH, PH>::OCC,
-                                              SplitConfig<D, NT, HKV, NWH, PH>::OCC)))
+                          amdgpu_waves_per_eu(SplitConfig<D, NT, HKV, NWH, PH, RS>::OCC,
+                                              SplitConfig<D, NT, HKV, NWH, PH, RS>::OCC)))
 void decode_split_kernel(DecodeArgs a) {
   static_assert(D == 128, "split-kernel instances are 128-dim (head dim 256 runs as paired halves)");
   using S = Slot<D>;
-  using CFG = SplitConfig<D, NT, HKV, NWH, PH>;
+  using CFG = SplitConfig<D, NT, HKV, NWH, PH, RS>;
   constexpr int KS = S::KS, DG = S::DG, RK = CFG::RK, RV = CFG::RV;
   __shared__ __attribute__((aligned(16))) char lds_raw[CFG::LDS_BYTES];
   lds_t *lds = (lds_t *)(lds_raw);
@@ -1093,6 +1101,9 @@ void decode_split_kernel(DecodeArgs a) {
   const int hq = PH ? h >> 1 : h;  // head of the query rows, scale planes and split state
   const int half = PH ? h & 1 : 0;
   const int n = lane & 15, g = lane >> 4;
+  // Row tile of the launch held in this wave's tile slot j (RS: alternate
+  // tiles w, w + 2; otherwise all NT).
+  auto tile_of = [&](int j) { return RS ? w + 2 * j : j; };
 
   const int role = static_cast<int>(blockIdx.x);  // this work-group's split of the plan
   const SplitPlan plan = plan_split(a, lane, role);
@@ -1129,7 +1140,7 @@ void decode_split_kernel(DecodeArgs a) {
       min_end = min(min_end, e);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const int r = r0 + 16 * nt + n;
+        const int r = r0 + 16 * tile_of(nt) + n;
         if (r < rows && r / kGqa == j) st.lim[nt] = min(e, L0);
       }
     }
@@ -1157,7 +1168,30 @@ void decode_split_kernel(DecodeArgs a) {
   // count of this wave's own loads.  Rows past the last query row load row 0
   // and are zeroed below.
   lds_t *qstage = kring + S::K_BYTES;
-  if (!PH && !pre_q) {
+  // RS: this wave's rows (its NT alternate tiles) come into registers instead
+  // (the ring's K slots are all needed), ahead of the table entries likewise;
+  // lane (n, g) takes row 16 tile + n, dims 64 ks + 16 g .. + 15.
+  v4i qraw[RS ? NT : 1][KS][2];
+  if constexpr (RS) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qraw[j][ks][0] = qraw[j][ks][1] = (v4i){0, 0, 0, 0};
+      const int r = r0 + 16 * tile_of(j) + n;
+      if (r < rows && !pre_q) {
+        const int jt = r / kGqa;
+        const int qh = h * kGqa + (r - jt * kGqa);
+        const uint16_t *src = a.q + (static_cast<int64_t>(b) * a.q_len + jt) * a.q_tok_stride +
+                              static_cast<int64_t>(qh) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          qraw[j][ks][0] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g);
+          qraw[j][ks][1] = *reinterpret_cast<const v4i *>(src + 64 * ks + 16 * g + 8);
+        }
+      }
+    }
+  }
+  if (!PH && !RS && !pre_q) {
     constexpr int RPD = 1024 / (2 * D);  // query rows per 1 KB load
     const char *qbase = reinterpret_cast<const char *>(a.q) + static_cast<int64_t>(b) * a.q_len * a.q_tok_stride * 2;
 #pragma unroll
@@ -1254,8 +1288,17 @@ void decode_split_kernel(DecodeArgs a) {
   // rest of theirs after the quantization.  (Issuing the whole ring first,
   // with the query rows in registers, was neutral at 4 x 131,072 tokens and
   // 0.1-0.4 us slower per step on short contexts.)
+  if constexpr (RS) {
+    // The query words came with the table entries: a use of them here puts
+    // the compiler's wait for them before the ring loads (inline assembly it
+    // does not count) instead of before the quantization.
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qraw[j][ks][0]), "v"(qraw[j][ks][1]));
+  }
   fill_slot(0);
-  if constexpr (PH) {
+  if constexpr (PH || RS) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
   }
@@ -1284,8 +1327,9 @@ void decode_split_kernel(DecodeArgs a) {
     const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(hq) * kPage * DQ;
     const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + hq * kPage;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < CFG::NTQ; ++nt) {
       if (nt % NWH != w) continue;
+      const int jl = RS ? nt / NWH : nt;  // this wave's tile slot
       const int r = r0 + 16 * nt + n;
       const bool live = r < rows;
 #pragma unroll
@@ -1296,23 +1340,30 @@ void decode_split_kernel(DecodeArgs a) {
         *reinterpret_cast<__attribute__((address_space(3))) v4i *>(qlds + ((nt * KSQ + ks) * kWave + lane) * 16) = frag;
       }
       const double c = static_cast<double>(live ? scales[r] : 0.f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(DQ)));
-      st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+      st.crow[jl] = fmaxf(static_cast<float>(c), 1e-30f);
       if (g == 0 && half == 0)
-        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
+        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[jl];
     }
   } else if constexpr (!PH) {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < CFG::NTQ; ++nt) {
       if (nt % NWH != w) continue;  // the partner wave quantizes this tile
+      const int jl = RS ? nt / NWH : nt;  // this wave's tile slot
       const bool live = r0 + 16 * nt + n < rows;
       float x[KS][16];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const v4i zero = {0, 0, 0, 0};
-        const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
-        const v4i w0 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row) : zero;
-        const v4i w1 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16) : zero;
+        v4i w0, w1;
+        if constexpr (RS) {
+          w0 = live ? qraw[jl][ks][0] : zero;
+          w1 = live ? qraw[jl][ks][1] : zero;
+        } else {
+          const lds_t *row = qstage + ((nt / NWH) * 16 + n) * 2 * D + 2 * (64 * ks + 16 * g);
+          w0 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row) : zero;
+          w1 = live ? *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(row + 16) : zero;
+        }
         const uint32_t words[8] = {static_cast<uint32_t>(w0[0]), static_cast<uint32_t>(w0[1]),
                                    static_cast<uint32_t>(w0[2]), static_cast<uint32_t>(w0[3]),
                                    static_cast<uint32_t>(w1[0]), static_cast<uint32_t>(w1[1]),
@@ -1344,21 +1395,21 @@ void decode_split_kernel(DecodeArgs a) {
       // score * log2(e) = dot * q_scale * k_scale * log2(e) / sqrt(D); kept > 0
       // so masked (-inf) scores never meet a zero factor.
       const double c = scale * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(D)));
-      st.crow[nt] = fmaxf(static_cast<float>(c), 1e-30f);
+      st.crow[jl] = fmaxf(static_cast<float>(c), 1e-30f);
       if (g == 0)
-        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[nt];
+        reinterpret_cast<__attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n] = st.crow[jl];
     }
   }
 
   // The staged query rows have been read (their values are quantized).
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  if constexpr (!PH) {
+  if constexpr (!PH && !RS) {
 #pragma unroll
     for (int s = 1; s < (RK > RV ? RK : RV); ++s) fill_slot(s);
   }
 
-  lds_int *flags = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);  // PH: ready[WAVES] | done[WAVES]
-  if constexpr (PH) {
+  lds_int *flags = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);  // PH, RS: ready[WAVES] | done[WAVES]
+  if constexpr (PH || RS) {
     pair_flag_set(flags + wave, 0, lane);
     pair_flag_set(flags + CFG::WAVES + wave, 0, lane);
   }
@@ -1370,7 +1421,8 @@ void decode_split_kernel(DecodeArgs a) {
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float f = reinterpret_cast<const __attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[nt * 16 + n];
+      const float f =
+          reinterpret_cast<const __attribute__((address_space(3))) float *>(qlds + CFG::Q_FRAG_BYTES)[tile_of(nt) * 16 + n];
       if constexpr (PH) {
         // f is the row's quantization scale (dead rows: zero operands, any factor)
         const double c = static_cast<double>(f) * (static_cast<double>(kLog2e) / sqrt(static_cast<double>(CFG::DQ)));
@@ -1400,6 +1452,67 @@ void decode_split_kernel(DecodeArgs a) {
   // paired halves are coupled per chunk already and run worse with it.
   lds_int *prog = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);
   if constexpr (CFG::BALANCE) pair_flag_set(prog + wave, 0, lane);
+  if constexpr (RS) {
+    // Row split: both waves of the head multiply every chunk of the split,
+    // in order; chunk c sits in the ring of wave c % 2 (its (c / 2)-th own
+    // chunk).  The owner publishes a chunk once its loads landed ("ready",
+    // counted in own chunks), each wave publishes the chunks it has finished
+    // reading ("done"), and the owner refills a slot only after both read
+    // it, so each chunk is fetched from HBM once.  Neither wave waits before
+    // publishing what the other waits for, so every wait ends.
+    const int pw = wave ^ HKV;  // the head's other wave
+    lds_t *pkring = lds + pw * CFG::WAVE_BYTES;
+    lds_t *pvring = pkring + RK * S::K_BYTES;
+    const int nall = max(0, x1 - x0);
+    for (int c = 0; c < nall; ++c) {
+      const bool own = (c & 1) == w;  // wave-uniform
+      const int ko = c >> 1;          // the owner's chunk count
+      const int sk = ko % RK, sv = ko % RV;
+      if (own) {
+        int mks = mk[0], mvs = mv[0];
+#pragma unroll
+        for (int s = 1; s < RK; ++s)
+          if (sk == s) mks = mk[s];
+#pragma unroll
+        for (int s = 1; s < RV; ++s)
+          if (sv == s) mvs = mv[s];
+        wait_vm(issued - max(mks, mvs));
+        pair_flag_set(flags + wave, ko + 1, lane);
+      } else {
+        pair_flag_wait(flags + pw, ko + 1, lane);
+      }
+      const lds_t *kslot = (own ? kring : pkring) + sk * S::K_BYTES;
+      const lds_t *vslot = (own ? vring : pvring) + sv * S::V_BYTES;
+      const int x = x0 + c;
+      const bool valid = page_of(x) >= 0;
+      const int tbase = 32 * x;
+      v4i sc[2][NT];
+      if (valid) chunk_qk<D, NT, 2>(kslot, qlds + w * KS * kWave * 16, lane, g, sc);
+      if (valid) chunk_softmax_pv<D, NT, false>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+      // This chunk's K and V slots have been read.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      pair_flag_set(flags + CFG::WAVES + wave, c + 1, lane);
+      if (own && (ko + RK < cnt || ko + RV < cnt)) {
+        pair_flag_wait(flags + CFG::WAVES + pw, c + 1, lane);
+        if (ko + RK < cnt) {
+          const int xr = my0 + (ko + RK) * NWH;
+          issue_k<D, HKV>(a, page_of(xr), xr, lo, kring + sk * S::K_BYTES);
+          issued += S::NK;
+#pragma unroll
+          for (int s = 0; s < RK; ++s)
+            if (sk == s) mk[s] = issued;
+        }
+        if (ko + RV < cnt) {
+          const int xr = my0 + (ko + RV) * NWH;
+          issue_v<D, HKV, false>(a, page_of(xr), xr, lo, lane, vring + sv * S::V_BYTES);
+          issued += S::NVS;
+#pragma unroll
+          for (int s = 0; s < RV; ++s)
+            if (sv == s) mv[s] = issued;
+        }
+      }
+    }
+  } else
   for (int k = 0; k < cnt; ++k) {
     const int sk = k % RK, sv = k % RV;  // wave-uniform ring slots
     if constexpr (CFG::BALANCE) {
@@ -1485,7 +1598,8 @@ void decode_split_kernel(DecodeArgs a) {
   finalize_output(st);
 
   // ---- combine the NWH waves of each head, then write the split state
-  if constexpr (NWH > 1) {
+  // (RS: each wave holds whole rows and writes them itself)
+  if constexpr (NWH > 1 && !RS) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __syncthreads();  // every ring is drained; reuse the LDS for the exchange
     float *xb = reinterpret_cast<float *>(lds_raw) + h * (CFG::XCHG_FLOATS);
@@ -1548,7 +1662,7 @@ void decode_split_kernel(DecodeArgs a) {
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = r0 + 16 * nt + 4 * g + i;
+      const int r = r0 + 16 * tile_of(nt) + 4 * g + i;
       const float m_r = __shfl(st.m_run[nt], 4 * g + i, kWave);  // row r's max sits in lane n = 4 g + i
       if (r < rows) {
         const float l = st.lsum[nt][i];
@@ -1568,10 +1682,9 @@ void decode_split_kernel(DecodeArgs a) {
   }
 }
 
-// Two waves per 128-dim head, each holding up to three row tiles: four
-// tiles (q_len 9-10) run as a launch of three (rows 0-47) and one of one
-// (rows 48-63) over the same plan, writing disjoint rows of the same split
-// states; the second launch re-reads pages the first left in the MALL.
+// Two waves per 128-dim head, each holding up to three row tiles; four
+// tiles (q_len 9-10) run split by rows (each wave two alternate tiles over
+// every chunk, the chunks shared between the two waves' rings).
 template <int HKV>
 void launch_split(DecodeArgs a, int nt, hipStream_t s) {
   const dim3 grid(a.grid), block(128 * HKV);
@@ -1580,11 +1693,7 @@ void launch_split(DecodeArgs a, int nt, hipStream_t s) {
     case 1: decode_split_kernel<128, 1, HKV, 2><<<grid, block, 0, s>>>(a); break;
     case 2: decode_split_kernel<128, 2, HKV, 2><<<grid, block, 0, s>>>(a); break;
     case 3: decode_split_kernel<128, 3, HKV, 2><<<grid, block, 0, s>>>(a); break;
-    default:
-      decode_split_kernel<128, 3, HKV, 2><<<grid, block, 0, s>>>(a);
-      a.tile0 = 3;
-      decode_split_kernel<128, 1, HKV, 2><<<grid, block, 0, s>>>(a);
-      break;
+    default: decode_split_kernel<128, 2, HKV, 2, false, true><<<grid, block, 0, s>>>(a); break;
   }
 }
 
