@@ -16,8 +16,10 @@
 //  * A work-group holds two waves per KV head (one per half-head with four
 //    256-dim heads), two per SIMD.  The waves of a head share the 6*q_len
 //    query rows of their head (int8-quantized in the prologue, padded to
-//    16-row tiles, up to three tiles per launch) as MFMA operands in LDS, so
-//    each K/V byte is fetched from HBM once and used for every GQA row.
+//    16-row tiles) as MFMA operands in LDS, so each K/V byte is fetched from
+//    HBM once and used for every GQA row.  With up to three tiles the two
+//    waves take alternate chunks; with four (q_len 9-10) each takes two
+//    tiles and both multiply every chunk, shared between their rings.
 //  * Each wave owns a ring of LDS slots filled by direct-to-LDS loads
 //    (global_load_lds, nontemporal for K and V): one slot is one 32-token
 //    chunk of its head (K rows with XOR-swizzled 16-byte chunks, V rows in a
