@@ -45,6 +45,39 @@ def test_decode_matches_oracle_small(gpu_ops, hkv, d, q_len):
     print("  max abs err %.2e" % err, flush=True)
 
 
+@pytest.mark.parametrize("hkv,q_len", [(4, 9), (2, 10)])
+def test_row_split_handles_odd_chunk_counts_tiny_splits_and_visible_ends(gpu_ops, hkv, q_len):
+    """Four row tiles (q_len 9-10) at 128 dims run split by rows: both waves
+    of a head multiply every chunk, each chunk in the ring of the wave that
+    loaded it.  Lengths with odd chunk counts, a one-chunk split, pages of
+    two 64-token halves, a 33-page manager block, explicit visible ends out
+    of order, and split counts from the default down to single pages."""
+    print("row split hkv=%d q=%d" % (hkv, q_len), flush=True)
+    lay = PageLayout(hkv, 128)
+    gen = torch.Generator().manual_seed(900 + 10 * hkv + q_len)
+    lengths = [1, 31, 32, 33, 95, 2113, 4097]
+    ppb = 3
+    table = random_tables(gen, lengths, 150, ppb=ppb)
+    cache = Cache(150, lay)
+    for b, L in enumerate(lengths):
+        fill_sequence(gpu_ops, cache, gen, table[b], L, ppb=ppb)
+    seq = torch.tensor(lengths, dtype=torch.int32)
+    q = seeded_normal(gen, (len(lengths) * q_len, lay.hq, 128))
+    want = _oracle(cache, q, table, seq, q_len, ppb=ppb)
+    for splits in (0, 7, 80):
+        got = decode(gpu_ops, cache, q, table, seq, q_len, ppb=ppb, num_splits=splits).float().cpu().numpy()
+        assert_close(got, want, what="row split, %d splits" % splits)
+    # Explicit ends out of causal order (tree verification): every row of a
+    # token sees its own count of keys, down to one.
+    vis = torch.zeros((len(lengths), 1 + q_len), dtype=torch.int32)
+    for b, L in enumerate(lengths):
+        vis[b, 0] = L
+        ends = torch.randint(1, L + 1, (q_len,), generator=gen, dtype=torch.int32)
+        vis[b, 1:] = ends
+    got = decode(gpu_ops, cache, q, table, seq, q_len, ppb=ppb, visible=vis).float().cpu().numpy()
+    assert_close(got, _oracle(cache, q, table, seq, q_len, ppb=ppb, visible=vis), what="row split, explicit ends")
+
+
 def test_decode_config1_exact_shape(gpu_ops):
     """1 sequence, context 2,048, q=1, 24/4 heads, D=128, table = randperm(64)[:32]."""
     lay = PageLayout(4, 128)
