@@ -28,3 +28,20 @@ def gpu_ops():
     from k8v4_v030.ops_api import ops
 
     return ops()
+
+
+@pytest.fixture(autouse=True)
+def _no_decode_wait_gave_up(request):
+    """Every GPU test: no in-kernel wait of the decode kernels (the handshakes
+    of the paired halves and of the row split) gave up while it ran; a wait
+    that gives up lets its wave go on, so it could hide in a tolerance."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    from k8v4_v030 import ops_api
+
+    lib = ops_api.load_library()
+    before = lib.k8v4_decode_fault_count()
+    yield
+    after = lib.k8v4_decode_fault_count()
+    assert after == before, "%d in-kernel decode waits gave up during the test" % (after - before)
