@@ -777,7 +777,7 @@ __device__ __forceinline__ void chunk_qk(const lds_t *kslot, const lds_t *qlds, 
 // LDS.  Same score layout and bias as chunk_qk; |dot| <= 256 * 127 * 127 <
 // 2^22 keeps the biased accumulator exact.  The two halves' K operands are
 // read one half at a time (16 registers instead of 32).
-template <int NT>
+template <int NT, int TS = 1>
 __device__ __forceinline__ void chunk_qk_pair(const lds_t *klo, const lds_t *khi, const lds_t *qlds, int lane, int g,
                                               v4i (&sc)[2][NT]) {
   const int n = lane & 15;
@@ -802,7 +802,7 @@ __device__ __forceinline__ void chunk_qk_pair(const lds_t *klo, const lds_t *khi
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const v4i qf = *reinterpret_cast<const __attribute__((address_space(3))) v4i *>(
-            qlds + ((nt * 4 + 2 * part + ks) * kWave + lane) * 16);
+            qlds + ((nt * TS * 4 + 2 * part + ks) * kWave + lane) * 16);
 #pragma unroll
         for (int ml = 0; ml < 2; ++ml) sc[ml][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[ml][ks], qf, sc[ml][nt], 0, 0, 0);
       }
@@ -1066,7 +1066,7 @@ struct SplitConfig {
   static constexpr int OCC = HKV > 4 ? HKV * NWH / 4 : NWH;  // waves per SIMD the kernel is built for
   static_assert(LDS_BYTES <= LDS_MAX, "decode ring exceeds the LDS");
   static_assert(PH || NWH == 2, "128-dim heads run two waves each");
-  static_assert(!RS || (!PH && NWH == 2), "row split: two waves per 128-dim head");
+  static_assert(!RS || NWH == 2, "row split: two waves per (half-)head");
   // The query rows of a wave's tiles are staged in its K slots 1..RK-1 (RS:
   // loaded into registers instead).
   static_assert(PH || RS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
@@ -1173,8 +1173,8 @@ void decode_split_kernel(DecodeArgs a) {
   // RS: this wave's rows (its NT alternate tiles) come into registers instead
   // (the ring's K slots are all needed), ahead of the table entries likewise;
   // lane (n, g) takes row 16 tile + n, dims 64 ks + 16 g .. + 15.
-  v4i qraw[RS ? NT : 1][KS][2];
-  if constexpr (RS) {
+  v4i qraw[RS && !PH ? NT : 1][KS][2];
+  if constexpr (RS && !PH) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
 #pragma unroll
@@ -1220,7 +1220,7 @@ void decode_split_kernel(DecodeArgs a) {
     constexpr int DQ = CFG::DQ, KSQ = DQ / 64;
     const int8_t *tile = a.q8 + static_cast<int64_t>(b) * a.q8_seq_stride + static_cast<int64_t>(hq) * kPage * DQ;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < CFG::NTQ; ++nt) {
       if (nt % NWH != w) continue;
 #pragma unroll
       for (int ks = 2 * half; ks < 2 * half + 2; ++ks) {
@@ -1231,7 +1231,7 @@ void decode_split_kernel(DecodeArgs a) {
     }
     if (w == 0 && half == 0) {
       const float *scales = a.q8_scale + static_cast<int64_t>(b) * a.qs_seq_stride + hq * kPage;
-      if (lane < NT * 16) dma4s(scales, static_cast<uint32_t>((r0 + lane) * 4), qlds + CFG::Q_FRAG_BYTES);
+      if (lane < CFG::NTQ * 16) dma4s(scales, static_cast<uint32_t>((r0 + lane) * 4), qlds + CFG::Q_FRAG_BYTES);
       ++issued;
     }
   }
@@ -1290,7 +1290,7 @@ void decode_split_kernel(DecodeArgs a) {
   // rest of theirs after the quantization.  (Issuing the whole ring first,
   // with the query rows in registers, was neutral at 4 x 131,072 tokens and
   // 0.1-0.4 us slower per step on short contexts.)
-  if constexpr (RS) {
+  if constexpr (RS && !PH) {
     // The query words came with the table entries: a use of them here puts
     // the compiler's wait for them before the ring loads (inline assembly it
     // does not count) instead of before the quantization.
@@ -1314,7 +1314,7 @@ void decode_split_kernel(DecodeArgs a) {
     // anything in its padding rows).
     constexpr int KSQ = CFG::DQ / 64;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < CFG::NTQ; ++nt) {
       if (nt % NWH != w || r0 + 16 * nt + n < rows) continue;
 #pragma unroll
       for (int ks = 2 * half; ks < 2 * half + 2; ++ks)
@@ -1455,20 +1455,21 @@ void decode_split_kernel(DecodeArgs a) {
   lds_int *prog = reinterpret_cast<lds_int *>(lds + CFG::FLAG_OFF);
   if constexpr (CFG::BALANCE) pair_flag_set(prog + wave, 0, lane);
   if constexpr (RS) {
-    // Row split: both waves of the head multiply every chunk of the split,
-    // in order; chunk c sits in the ring of wave c % 2 (its (c / 2)-th own
-    // chunk).  The owner publishes a chunk once its loads landed ("ready",
-    // counted in own chunks), each wave publishes the chunks it has finished
-    // reading ("done"), and the owner refills a slot only after both read
-    // it, so each chunk is fetched from HBM once.  Neither wave waits before
-    // publishing what the other waits for, so every wait ends.
-    const int pw = wave ^ HKV;  // the head's other wave
-    lds_t *pkring = lds + pw * CFG::WAVE_BYTES;
-    lds_t *pvring = pkring + RK * S::K_BYTES;
+    // Row split: both waves of the head (of each half-head, PH) multiply
+    // every chunk of the split, in order; chunk c sits in the rings of the
+    // waves with w = c % 2 (their (c / 2)-th own chunk; PH: its K halves in
+    // the two half-head waves, each V half in its own).  An owner publishes a
+    // chunk once its loads landed ("ready", counted in own chunks), every
+    // wave publishes the chunks it has finished reading ("done"), and an
+    // owner refills a slot only after every wave that reads it did, so each
+    // chunk is fetched from HBM once.  No wave waits before publishing what
+    // the others wait for, so every wait ends.
+    const int hb = PH ? (h & ~1) : h;  // first (half-)head wave of this head
     const int nall = max(0, x1 - x0);
     for (int c = 0; c < nall; ++c) {
-      const bool own = (c & 1) == w;  // wave-uniform
-      const int ko = c >> 1;          // the owner's chunk count
+      const int wo = c & 1;            // w of the chunk's owners
+      const bool own = wo == w;        // wave-uniform
+      const int ko = c >> 1;           // the owners' chunk count
       const int sk = ko % RK, sv = ko % RV;
       if (own) {
         int mks = mk[0], mvs = mv[0];
@@ -1480,22 +1481,42 @@ void decode_split_kernel(DecodeArgs a) {
           if (sv == s) mvs = mv[s];
         wait_vm(issued - max(mks, mvs));
         pair_flag_set(flags + wave, ko + 1, lane);
-      } else {
-        pair_flag_wait(flags + pw, ko + 1, lane);
       }
-      const lds_t *kslot = (own ? kring : pkring) + sk * S::K_BYTES;
-      const lds_t *vslot = (own ? vring : pvring) + sv * S::V_BYTES;
+      const int ow = wo * HKV;         // owner waves: ow + hb (+ 1 for PH)
+      if constexpr (PH) {
+        pair_flag_wait(flags + ow + hb, ko + 1, lane);
+        pair_flag_wait(flags + ow + hb + 1, ko + 1, lane);
+      } else {
+        if (!own) pair_flag_wait(flags + ow + h, ko + 1, lane);
+      }
+      const lds_t *vslot = lds + (ow + h) * CFG::WAVE_BYTES + RK * S::K_BYTES + sv * S::V_BYTES;
       const int x = x0 + c;
       const bool valid = page_of(x) >= 0;
       const int tbase = 32 * x;
       v4i sc[2][NT];
-      if (valid) chunk_qk<D, NT, 2>(kslot, qlds + w * KS * kWave * 16, lane, g, sc);
-      if (valid) chunk_softmax_pv<D, NT, false>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
+      if constexpr (PH) {
+        const lds_t *klo = lds + (ow + hb) * CFG::WAVE_BYTES + sk * S::K_BYTES;
+        const lds_t *khi = lds + (ow + hb + 1) * CFG::WAVE_BYTES + sk * S::K_BYTES;
+        if (valid) chunk_qk_pair<NT, 2>(klo, khi, qlds + w * 4 * kWave * 16, lane, g, sc);
+      } else {
+        const lds_t *kslot = lds + (ow + h) * CFG::WAVE_BYTES + sk * S::K_BYTES;
+        if (valid) chunk_qk<D, NT, 2>(kslot, qlds + w * KS * kWave * 16, lane, g, sc);
+      }
+      if (valid) chunk_softmax_pv<D, NT, PH>(st, sc, vslot, tbase, L0, lane, g, tbase + 32 > min_end);
       // This chunk's K and V slots have been read.
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       pair_flag_set(flags + CFG::WAVES + wave, c + 1, lane);
       if (own && (ko + RK < cnt || ko + RV < cnt)) {
-        pair_flag_wait(flags + CFG::WAVES + pw, c + 1, lane);
+        // Every reader of this wave's slots is done with chunk c: the head's
+        // other w (PH: both its half-head waves) and, PH, the other half.
+        const int xw = (1 - w) * HKV;
+        if constexpr (PH) {
+          pair_flag_wait(flags + CFG::WAVES + xw + hb, c + 1, lane);
+          pair_flag_wait(flags + CFG::WAVES + xw + hb + 1, c + 1, lane);
+          pair_flag_wait(flags + CFG::WAVES + (wave ^ 1), c + 1, lane);
+        } else {
+          pair_flag_wait(flags + CFG::WAVES + xw + h, c + 1, lane);
+        }
         if (ko + RK < cnt) {
           const int xr = my0 + (ko + RK) * NWH;
           issue_k<D, HKV>(a, page_of(xr), xr, lo, kring + sk * S::K_BYTES);
@@ -1506,7 +1527,7 @@ void decode_split_kernel(DecodeArgs a) {
         }
         if (ko + RV < cnt) {
           const int xr = my0 + (ko + RV) * NWH;
-          issue_v<D, HKV, false>(a, page_of(xr), xr, lo, lane, vring + sv * S::V_BYTES);
+          issue_v<D, HKV, PH>(a, page_of(xr), xr, lo, lane, vring + sv * S::V_BYTES);
           issued += S::NVS;
 #pragma unroll
           for (int s = 0; s < RV; ++s)
@@ -1727,11 +1748,7 @@ void launch_split_pairs(DecodeArgs a, int nt, int hkv, hipStream_t s) {
     case 1: decode_split_kernel<128, 1, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
     case 2: decode_split_kernel<128, 2, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
     case 3: decode_split_kernel<128, 3, 4, 2, true><<<grid, dim3(512), 0, s>>>(a); break;
-    default:
-      decode_split_kernel<128, 3, 4, 2, true><<<grid, dim3(512), 0, s>>>(a);
-      a.tile0 = 3;
-      decode_split_kernel<128, 1, 4, 2, true><<<grid, dim3(512), 0, s>>>(a);
-      break;
+    default: decode_split_kernel<128, 2, 4, 2, true, true><<<grid, dim3(512), 0, s>>>(a); break;
   }
 }
 
