@@ -289,6 +289,12 @@ int64_t k8v4_decode_fault_count(void);
  * gathered K/V per head inside the call, onednn_prefill.py:226-239). */
 int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, int hkv, int head_dim);
 
+/* Whether k8v4_prefill_paged serves this shape from per-KV-head tile images
+ * (each page dequantized once per head; 1), or converts pages in place as
+ * k8v4_prefill_paged_batch does (0); -1 on bad arguments.  No counterpart in
+ * the reference: a caller batching a step's chunks sends the former alone. */
+int k8v4_prefill_uses_tiles(int64_t seq_len, int64_t q_len, int hkv, int head_dim);
+
 /* Workspace bytes k8v4_attn_batch needs for this shape (-1 on bad arguments).
  * No counterpart in the reference (its caller sized [nprog, 64, D] fp32
  * partials, k8v4_v030/scratch.py:34-45, which is always at least this). */

@@ -1587,6 +1587,15 @@ extern "C" int64_t k8v4_prefill_workspace_bytes(int64_t seq_len, int64_t q_len, 
   return workspace_need(pl, seq_len, head_dim);
 }
 
+extern "C" int k8v4_prefill_uses_tiles(int64_t seq_len, int64_t q_len, int hkv, int head_dim) {
+  using namespace k8v4;
+  if (!supported_heads(hkv) || !supported_dim(head_dim) || q_len < 0 || q_len > seq_len) return -1;
+  if (q_len == 0) return 0;
+  PrefillPlan pl;
+  if (!plan_prefill(seq_len, q_len, hkv, head_dim, pl)) return -1;
+  return use_tiles(pl, head_dim) ? 1 : 0;
+}
+
 extern "C" int k8v4_prefill_paged(const void *q, int q_dtype, int64_t q_tok_stride, const int8_t *k_cache,
                                   const float *k_scale, const uint8_t *v_cache, const float *v_scale,
                                   const float *v_zero, int64_t num_pages, int64_t k_page_stride,

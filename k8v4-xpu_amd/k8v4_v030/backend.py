@@ -346,13 +346,9 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
 # gain nothing from running alone: a step's share one batched launch.  A chunk
 # the single entry serves from per-head tile images (each page dequantized
 # once per KV head: at head dim 128 over 128 tokens; at head dim 256 long
-# chunks over long contexts) runs alone.  The library's plan decides; its
-# workspace shows the choice (tile images beyond the batched launch's
-# partial states).
+# chunks over long contexts) runs alone.  The library's plan decides.
 def _runs_alone(width: int, seq_len: int, layout) -> bool:
-    o = ops()
-    return (o.prefill_workspace_bytes(seq_len, width, layout.hkv, layout.head_dim)
-            > o.prefill_batch_workspace_bytes(layout.hkv, layout.head_dim))
+    return ops().prefill_uses_tiles(seq_len, width, layout.hkv, layout.head_dim)
 
 
 def _check_covers(seq_len: int, width: int) -> None:

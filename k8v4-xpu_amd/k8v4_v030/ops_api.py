@@ -74,6 +74,7 @@ _EXTRA_SYMBOLS.append((
     _i32,
 ))
 _EXTRA_SYMBOLS.append(("k8v4_prefill_workspace_bytes", [_i64, _i64, _i32, _i32], _i64))
+_EXTRA_SYMBOLS.append(("k8v4_prefill_uses_tiles", [_i64, _i64, _i32, _i32], _i32))
 _EXTRA_SYMBOLS.append((
     "k8v4_prefill_paged_batch",
     [_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -363,6 +364,14 @@ class _Ops:
         n = int(self._lib.k8v4_prefill_workspace_bytes(int(seq_len), int(q_len), int(hkv), int(head_dim)))
         _require(n >= 0, "bad shape for the prefill workspace")
         return n
+
+    def prefill_uses_tiles(self, seq_len: int, q_len: int, hkv: int, head_dim: int) -> bool:
+        """Whether :meth:`prefill_paged` serves this shape from per-KV-head tile
+        images (each page dequantized once per head) rather than converting
+        pages in place as :meth:`prefill_paged_batch` does."""
+        n = int(self._lib.k8v4_prefill_uses_tiles(int(seq_len), int(q_len), int(hkv), int(head_dim)))
+        _require(n >= 0, "bad shape for the prefill plan")
+        return n == 1
 
     def prefill_paged(self, q, k_cache, k_scale, v_cache, v_scale, v_zero, block_row, seq_len: int,
                       pages_per_block: int, scale: float, out, workspace=None):

@@ -225,3 +225,24 @@ def test_prefill_batch_workspace_covers_every_short_single_call(lib):
             assert lib.k8v4_prefill_workspace_bytes(seq_len, q_len, hkv, d) <= need
     assert lib.k8v4_prefill_batch_workspace_bytes(3, 128) == -1
     assert lib.k8v4_prefill_batch_workspace_bytes(4, 64) == -1
+
+
+@pytest.mark.parametrize("hkv,d,q_len,ctx,tiles", [
+    # head dim 128: tile images from four 256-row blocks on (q_len > 128)
+    (4, 128, 128, 4096, False), (4, 128, 129, 4096, True), (2, 128, 4224, 131072, True),
+    # head dim 256: only where the per-head pre-pass pays for itself
+    (2, 256, 128, 4096, False), (2, 256, 512, 4096, False), (2, 256, 512, 16384, False),
+    (2, 256, 512, 65536, True), (2, 256, 2048, 16384, True), (2, 256, 4224, 131072, True),
+    (4, 256, 128, 65536, False), (4, 256, 4224, 65536, True),
+])
+def test_single_prefill_uses_tile_images_where_they_pay(lib, hkv, d, q_len, ctx, tiles):
+    """The single prefill entry's plan (the library's): pages dequantized once
+    per KV head into tile images beside the partial states, or converted in
+    place like the batched entry (the backend sends only the latter to one
+    batched launch)."""
+    seq_len = ctx + q_len
+    assert lib.k8v4_prefill_uses_tiles(seq_len, q_len, hkv, d) == int(tiles)
+    if tiles:  # the workspace holds one tile image per page beside the partial states
+        stride = 35 * 1024 if d == 128 else 68 * 1024
+        assert lib.k8v4_prefill_workspace_bytes(seq_len, q_len, hkv, d) > -(-seq_len // 64) * stride
+    assert lib.k8v4_prefill_uses_tiles(seq_len, seq_len + 1, hkv, d) == -1
