@@ -104,7 +104,7 @@ struct DecodeArgs {
   int grid;              // number of split work-groups (the plan's G)
   int min_pages;
   int merge_cs;   // column slices per output row in the merge
-  int tile0;      // first 16-row query tile of this split launch (D = 256, four tiles: two launches of two)
+  int tile0;      // first 16-row query tile of this split launch (four 256-dim heads, four tiles: three, then one)
   int units;      // merge units: output rows x merge_cs
   void *out;
   int out_dtype;
@@ -1158,9 +1158,10 @@ void decode_split_kernel(DecodeArgs a) {
   // instructions; mk[s] / mv[s] is the count right after the K / V group of
   // ring slot s was issued, so a chunk is resident once at most
   // issued - max(mk, mv) loads remain outstanding (loads complete in order).
-  // Only the first chunk's K and V groups go out before the quantization
-  // (register query words wait for every vector load issued before their
-  // first use); the rest of the ring is filled right after it.
+  // With the query rows staged in K slots 1.., only the first chunk's K and
+  // V groups go out before the quantization and the rest of the ring right
+  // after it; the paired halves and the row split (no staging) fill the
+  // whole ring at once.
   int issued = 0;
   // Q in LDS: this wave's query rows (its tiles nt = w, w + NWH, ...) go by
   // direct-to-LDS loads into its K slots 1.. (filled only after the
