@@ -1068,7 +1068,7 @@ struct SplitConfig {
   static_assert(PH || NWH == 2, "128-dim heads run two waves each");
   static_assert(!RS || NWH == 2, "row split: two waves per (half-)head");
   // The query rows of a wave's tiles are staged in its K slots 1..RK-1 (RS:
-  // loaded into registers instead).
+  // loaded into registers instead; PH: read already quantized).
   static_assert(PH || RS || ((NT + NWH - 1) / NWH) * 16 * 2 * D <= (RK - 1) * Slot<D>::K_BYTES,
                 "query staging does not fit the K ring");
 };
@@ -1404,7 +1404,8 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
 
-  // The staged query rows have been read (their values are quantized).
+  // Where the query rows were staged in K slots 1.., they have been read
+  // (their values are quantized) and those slots can take chunk data.
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   if constexpr (!PH && !RS) {
 #pragma unroll
