@@ -18,7 +18,8 @@ non-contiguous block tables.  Prints ONE JSON line:
   from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present;
 * ``cpu_baseline``: the reference's PyTorch path restated in torch
   (oracle/torch_cpu.py) on every host core: the whole headline decode step,
-  config 2's store and config 5's whole prefill chunk; the float64 oracle
+  config 2's store and config 5's whole prefill chunk, plus config 1's shape
+  through the pure-Python ``causal_gqa`` on one thread; the float64 oracle
   checks the GPU's headline output, the torch port the GPU's prefill output;
 * ``step_graph_us`` and the configs' ``graph_us_*``: per-launch time from HIP
   graphs of back-to-back launches replayed between two events (median and
@@ -420,7 +421,8 @@ def cpu_baseline(torch, work, store_work=None, prefill_work=None):
     decode: the whole headline step (4 x 131,072 tokens, q = 7) -- gather and
     dequantize, int8 query rows, fp32 attention; store: config 2's 16,896 tokens
     quantized into the cache (both median of 3 after one warm-up); prefill:
-    config 5's whole chunk over all 135,296 keys (key-tiled online softmax), once.
+    config 5's whole chunk over all 135,296 keys (key-tiled online softmax), once;
+    config 1's shape through the pure-Python ``causal_gqa``, one thread.
     The float64 oracle checks the GPU's headline output on the same cache."""
     import numpy as np
 
@@ -471,7 +473,27 @@ def cpu_baseline(torch, work, store_work=None, prefill_work=None):
         out["store"] = cpu_store_baseline(torch, store_work, torch_cpu, geom)
     if prefill_work is not None:
         out["prefill"] = cpu_prefill_baseline(torch, prefill_work, torch_cpu)
+    out["config1_scalar"] = cpu_scalar_baseline()
     return out
+
+
+def cpu_scalar_baseline():
+    """Config 1's shape (1 x 2,048 tokens, q = 1, 24 Q / 4 KV heads, D = 128)
+    through the pure-Python restatement of the reference's ``causal_gqa``
+    (oracle/scalar.py; reference oracle.py:140-162), which quantizes the K and V
+    rows itself: one thread, median of 3 after one warm-up, uniform rows."""
+    from oracle import scalar
+
+    seq, q_len, hq, hkv, dim = 2048, 1, 24, 4, 128
+    key = scalar.deterministic_rows(seq, hkv, 1, dim)
+    value = scalar.deterministic_rows(seq, hkv, 2, dim)
+    query = scalar.deterministic_rows(q_len, hq, 3, dim)
+    sec = median_seconds(lambda: scalar.causal_gqa(query, key, value, seq, q_len))
+    kv_bytes = seq * hkv * (dim + dim // 2 + 12)
+    return {"value": round(kv_bytes / sec / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "seconds": round(sec, 3), "us_per_layer": round(sec * 1e6, 1),
+            "sample": "config 1's shape through the pure-Python causal_gqa (quantizes 2,048 x 4 K and V rows, "
+                      "then int8-Q attention for 24 heads), one thread, median of 3 after 1 warm-up"}
 
 
 def cpu_store_baseline(torch, w, torch_cpu, geom):
