@@ -348,6 +348,7 @@ class Xe2K8V4Impl(AttentionImpl[Xe2K8V4Metadata]):
 # once per KV head: at head dim 128 over 128 tokens; at head dim 256 long
 # chunks over long contexts) runs alone.  The library's plan decides.
 def _runs_alone(width: int, seq_len: int, layout) -> bool:
+    _check_covers(seq_len, width)
     return ops().prefill_uses_tiles(seq_len, width, layout.hkv, layout.head_dim)
 
 

@@ -190,3 +190,13 @@ def test_scratch_covers_every_decode_call_the_engine_can_issue(hkv, head, max_mo
     assert ws is s.decode_ws and m is None and l is None and merged is None
     assert s.q8.shape == (hkv, 64, head) and s.q_scale.shape == (hkv, 64)  # created on first use
     clear_scratch()
+
+
+def test_prefill_plan_query_reports_a_short_sequence_length():
+    """A prefill whose sequence length does not include its own query tokens
+    is refused with the length message before any prefill launch is planned."""
+    lay = PageLayout(hkv=4, head_dim=128)
+    with pytest.raises(RuntimeError, match="seq_len 5 does not cover query 10"):
+        backend._runs_alone(10, 5, lay)
+    assert backend._runs_alone(4, 100, lay) is False
+    assert backend._runs_alone(2048, 4096, lay) is True
